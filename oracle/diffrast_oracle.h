@@ -1,0 +1,134 @@
+/*
+ * CPU oracle for the soft-triangle rasterizer hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
+ * CPU implementation (crates/diffrast/src/{raster,grad,canvas,optim,fit}.rs),
+ * used by tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py
+ * as the checker. The product (libdiffrast_hip.so and the Python package) never
+ * links, loads or calls it.
+ *
+ * Layouts follow the reference exactly:
+ *   params  : T x 10 floats per scene, [x0,y0,x1,y1,x2,y2,r,g,b,a]
+ *             (scene.rs:81-92), index 0 composited first (back).
+ *   images  : H x W x 3 floats, row-major, (y*W + x)*3 + ch (canvas.rs:27-29).
+ * Batched entry points take B consecutive scenes / images and B backgrounds.
+ */
+#ifndef DIFFRAST_ORACLE_H
+#define DIFFRAST_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Work counters for the roofline: pixels inside a live triangle's padded
+ * bounding box (n_box) and those whose weight passed MIN_WEIGHT (n_contrib). */
+typedef struct {
+    uint64_t n_box;
+    uint64_t n_contrib;
+} orc_counts;
+
+/* raster.rs:37-68 render(). counts may be NULL. */
+void orc_render(const float *params, size_t T, const float bg[3], size_t W,
+                size_t H, float sigma, float *out, orc_counts *counts);
+
+/* canvas.rs:45-58 Canvas::mse(). */
+float orc_mse(const float *a, const float *b, size_t n);
+
+/* grad.rs:56-131: render_with_tape + backward against a target.
+ * Returns the loss; writes T*10 grads. out_image (H*W*3) may be NULL. */
+float orc_loss_backward(const float *params, size_t T, const float bg[3],
+                        size_t W, size_t H, float sigma, const float *target,
+                        float *grads, float *out_image, orc_counts *counts);
+
+/* Upstream-gradient backward, the reference's CPU semantics
+ * (crates/diffrast-py/src/lib.rs:301-318): rebuild t = r - g*N/2 and run
+ * backward() against it. */
+void orc_backward_from_grad_inverted(const float *params, size_t T,
+                                     const float bg[3], size_t W, size_t H,
+                                     float sigma, const float *grad_image,
+                                     float *grads);
+
+/* Upstream-gradient backward with dL/dpixel taken as given, the semantics of
+ * the reference GPU path (backward_batch_reduced.wgsl:143-156). */
+void orc_backward_from_grad(const float *params, size_t T, const float bg[3],
+                            size_t W, size_t H, float sigma,
+                            const float *grad_image, float *grads);
+
+/* grad.rs:192-212: batch forms, one worker thread per item, results in input
+ * order (rayon par_iter). nthreads <= 0 means one per online CPU, capped at B. */
+void orc_render_batch(const float *params, size_t B, size_t T,
+                      const float *bgs, size_t W, size_t H, float sigma,
+                      float *out, int nthreads, orc_counts *counts);
+void orc_loss_backward_batch(const float *params, size_t B, size_t T,
+                             const float *bgs, size_t W, size_t H, float sigma,
+                             const float *targets, float *losses, float *grads,
+                             int nthreads, orc_counts *counts);
+void orc_backward_from_grad_batch(const float *params, size_t B, size_t T,
+                                  const float *bgs, size_t W, size_t H,
+                                  float sigma, const float *grad_images,
+                                  float *grads, int nthreads);
+
+/* grad.rs:298-323 finite_difference(): central differences of the loss. */
+float orc_finite_difference(const float *params, size_t T, const float bg[3],
+                            size_t W, size_t H, float sigma,
+                            const float *target, float eps, float *grads);
+
+/* optim.rs:40-60 Adam::step(). t is the step count before the call; the
+ * function increments it. */
+void orc_adam_step(float *params, const float *grads, const float *lr,
+                   float *m, float *v, uint32_t *t, size_t n, float beta1,
+                   float beta2, float eps);
+
+/* fit.rs:399-424 project(). n must be a multiple of 10. */
+void orc_project(float *params, size_t n);
+
+/* fit.rs:343-349 sigma_at(). */
+float orc_sigma_at(float sigma_start, float sigma_end, size_t iters, size_t i);
+
+/* fit.rs:49-65 FitConfig (patience < 0 means None). The initial scene is
+ * passed in: the reference draws it from rand::StdRng (fit.rs:217, 356-367),
+ * whose stream is not restated here. */
+typedef struct {
+    size_t iters;
+    float sigma_start, sigma_end;
+    float lr_pos, lr_color, lr_alpha;
+    long patience;
+    float min_delta;
+} orc_fit_config;
+
+enum { ORC_COMPLETED = 0, ORC_CONVERGED = 1, ORC_DIVERGED = 2 };
+
+typedef struct {
+    size_t n_losses;
+    size_t best_iter;
+    float best_loss;
+    int stop_reason;
+} orc_fit_report;
+
+/* fit.rs:166-288: the Fitter loop from a given initial scene. losses must hold
+ * cfg->iters floats; best_params T*10 floats. */
+void orc_fit(const float *target, size_t W, size_t H, const float bg[3],
+             const float *init_params, size_t T, const orc_fit_config *cfg,
+             float *losses, float *best_params, orc_fit_report *report);
+
+/* fit.rs:369-385 mean_color() and sample(), used by seed_scene(). */
+void orc_mean_color(const float *image, size_t W, size_t H, float out[3]);
+void orc_sample(const float *image, size_t W, size_t H, float x, float y,
+                float out[3]);
+
+/* Primitives exposed for the reference's unit tests (raster.rs:170-241,
+ * grad.rs:231-270). tri points at one 10-float triangle record. */
+float orc_signed_distance(const float *tri, float px, float py);
+float orc_coverage(const float *tri, float px, float py, float sigma);
+float orc_coverage_with_grad(const float *tri, float px, float py, float sigma,
+                             float dcov_dverts[6]);
+int orc_pixel_bounds(const float *tri, size_t W, size_t H, float sigma,
+                     uint64_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
