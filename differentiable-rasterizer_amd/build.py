@@ -1,0 +1,65 @@
+"""Builds libdiffrast_hip.so (gfx950) in-tree with hipcc.
+
+Usage: python build.py [--verbose]. The library lands next to this file, where
+`diffrast._lib` loads it from.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libdiffrast_hip.so"
+ARCH = os.environ.get("DIFFRAST_OFFLOAD_ARCH", "gfx950")
+
+SOURCES = [CSRC / "kernels.hip", CSRC / "runtime.hip"]
+HEADERS = [CSRC / "kernels.h", ROOT / "include" / "diffrast_hip.h"]
+
+# -ffp-contract=off: the kernels state every FMA explicitly; plain a*b+c must
+# round twice, as the reference's arithmetic does.
+# -packed-fp32-ops: no v_pk_*_f32 instructions in the generated code.
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose: bool = False) -> Path:
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, *map(str, SOURCES), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "packed-fp32-ops"
+    err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

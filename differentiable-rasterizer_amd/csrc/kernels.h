@@ -1,0 +1,72 @@
+// Shared definitions between the HIP kernels and the host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace drh {
+
+constexpr int NP = 10;    // parameters per triangle (scene.rs:21)
+constexpr int TILE = 8;   // a wave covers an 8x8 pixel tile, one pixel per lane
+constexpr int WAVES = 4;  // waves per block: 2x2 tiles, a 16x16 pixel region
+constexpr int CH = 128;   // triangles per chunk (LDS accumulators are per chunk)
+
+// Per-triangle record, REC floats, written by setup_records.
+constexpr int REC = 48;
+enum RecField : int {
+    R_V = 0,       // 6: vertices x0 y0 x1 y1 x2 y2
+    R_C = 6,       // 3: colour
+    R_A = 9,       // clamped alpha (NaN preserved)
+    R_BOX = 10,    // 4 ints: x0 y0 x1 y1, half-open; all 0 when not live
+    R_FLAGS = 14,  // int: F_*
+    R_SPARE = 15,
+    R_E = 16,      // 6: edge vectors b - a for (v0,v1) (v1,v2) (v2,v0)
+    R_LEN2 = 22,   // 3: |e|^2
+    R_RLEN2 = 25,  // 3: 1/|e|^2, 0 when |e|^2 <= 1e-20
+    R_N = 28,      // 6: outward unit normals (0 when the fast path is off)
+    R_OFF = 34,    // 3: a . n per edge
+    R_FAR = 37,    // max outward distance above which w < MIN_WEIGHT
+    R_DEEP = 38,   // max outward distance below which coverage == 1.0f
+};
+enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4 };
+
+enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2 };
+
+struct RasterArgs {
+    int B, T, H, W;
+    float sigma;
+    const float* rec;      // B*T*REC
+    const float* bg;       // B*3
+    const float* target;   // B*H*W*3 (MODE_LOSS)
+    const float* grad_in;  // B*H*W*3 (MODE_GRAD_IN)
+    float* out_img;        // B*H*W*3 (MODE_RENDER; optional in MODE_LOSS)
+    float* partials;       // B*nblk*T*NP
+    double* partial_loss;  // B*nblk
+};
+
+// Device-side state of a running fit (fit.rs:197-211).
+enum : int { STOP_COMPLETED = 0, STOP_CONVERGED = 1, STOP_DIVERGED = 2 };
+struct FitState {
+    float best_loss;
+    int best_iter;
+    int since;
+    int n_losses;
+    int stop;  // -1 while running, else STOP_*
+};
+
+dim3 raster_grid(int B, int W, int H);
+hipError_t launch_fit_tail(int iter, const float* loss, float* params, const float* grads, float* m, float* v,
+                           const float* lr, int n, float beta1, float beta2, float eps, float bc1, float bc2,
+                           float min_delta, long long patience, FitState* st, float* losses_out,
+                           float* best_params, hipStream_t s);
+
+hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
+                        float* rec, hipStream_t s);
+hipError_t launch_raster(int mode, bool fast, const RasterArgs& a, hipStream_t s);
+hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
+                         int npix3, float* grads, float* losses, hipStream_t s);
+hipError_t launch_adam(float* params, const float* grads, float* m, float* v, const float* lr, int n,
+                       float beta1, float beta2, float eps, float bc1, float bc2, int project,
+                       hipStream_t s);
+
+}  // namespace drh

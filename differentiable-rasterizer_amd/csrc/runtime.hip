@@ -1,0 +1,620 @@
+// Host runtime behind the C ABI in include/diffrast_hip.h: argument checks,
+// the device-buffer pool, host/device pointer staging, kernel sequencing and
+// the device-side fit loop.
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "diffrast_hip.h"
+#include "kernels.h"
+
+using drh::NP;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(DRH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                       \
+    do {                                          \
+        hipError_t _e = (expr);                   \
+        if (_e != hipSuccess) return hip_fail(_e, what); \
+    } while (0)
+
+// What a pooled buffer holds; part of the pool key so that, as in the
+// reference pool (crates/diffrast-gpu/src/lib.rs:132-143), a buffer is only
+// reused for the same purpose at exactly the same size.
+enum Kind : uint64_t {
+    K_REC = 1,
+    K_PARTIALS,
+    K_PLOSS,
+    K_IN_PARAMS,
+    K_IN_BG,
+    K_IN_IMAGES,
+    K_OUT_IMAGES,
+    K_OUT_GRADS,
+    K_OUT_LOSSES,
+    K_FIT_F32,
+    K_FIT_STATE,
+};
+
+// Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
+// released beyond it are freed.
+constexpr uint64_t POOL_BYTE_LIMIT = 512ull << 20;
+
+struct PoolBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t ev = nullptr;          // recorded when the last user released it
+    hipStream_t stream = nullptr;     // stream of that last use
+    bool used = false;
+};
+
+}  // namespace
+
+struct drh_ctx {
+    int device = 0;
+    bool discrete = true;
+    std::string info;
+    std::mutex mu;
+    std::unordered_map<uint64_t, std::vector<PoolBuf>> free_bufs;
+    uint64_t hits = 0, misses = 0, bytes = 0;
+};
+
+namespace {
+
+uint64_t pool_key(uint64_t kind, size_t bytes) { return (kind << 56) | (uint64_t)bytes; }
+
+// A buffer borrowed from the pool for the duration of one call. On release an
+// event is recorded on the stream, and a later user on a different stream
+// waits for it, so reuse never races queued work.
+class Lease {
+  public:
+    Lease() = default;
+    Lease(const Lease&) = delete;
+    Lease& operator=(const Lease&) = delete;
+    ~Lease() { release(); }
+
+    int acquire(drh_ctx* ctx, uint64_t kind, size_t bytes, hipStream_t s) {
+        ctx_ = ctx;
+        kind_ = kind;
+        stream_ = s;
+        if (bytes == 0) return DRH_OK;
+        {
+            std::lock_guard<std::mutex> g(ctx->mu);
+            auto it = ctx->free_bufs.find(pool_key(kind, bytes));
+            if (it != ctx->free_bufs.end() && !it->second.empty()) {
+                buf_ = it->second.back();
+                it->second.pop_back();
+                ctx->bytes -= bytes;
+                ctx->hits += 1;
+            }
+        }
+        if (buf_.ptr) {
+            if (buf_.used && buf_.stream != s) {
+                hipError_t e = hipStreamWaitEvent(s, buf_.ev, 0);
+                if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+            }
+            return DRH_OK;
+        }
+        {
+            std::lock_guard<std::mutex> g(ctx->mu);
+            ctx->misses += 1;
+        }
+        hipError_t e = hipMalloc(&buf_.ptr, bytes);
+        if (e != hipSuccess) {
+            buf_.ptr = nullptr;
+            return fail(e == hipErrorOutOfMemory ? DRH_ERR_TOO_LARGE : DRH_ERR_DEVICE,
+                        std::string("hipMalloc of ") + std::to_string(bytes) + " bytes: " + hipGetErrorString(e));
+        }
+        buf_.bytes = bytes;
+        e = hipEventCreateWithFlags(&buf_.ev, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+        return DRH_OK;
+    }
+
+    template <class T>
+    T* get() const {
+        return static_cast<T*>(buf_.ptr);
+    }
+
+    void release() {
+        if (!buf_.ptr) return;
+        (void)hipEventRecord(buf_.ev, stream_);
+        buf_.stream = stream_;
+        buf_.used = true;
+        bool keep = false;
+        {
+            std::lock_guard<std::mutex> g(ctx_->mu);
+            if (ctx_->bytes + buf_.bytes <= POOL_BYTE_LIMIT) {
+                ctx_->bytes += buf_.bytes;
+                ctx_->free_bufs[pool_key(kind_, buf_.bytes)].push_back(buf_);
+                keep = true;
+            }
+        }
+        if (!keep) {
+            (void)hipEventSynchronize(buf_.ev);
+            (void)hipEventDestroy(buf_.ev);
+            (void)hipFree(buf_.ptr);
+        }
+        buf_ = PoolBuf{};
+    }
+
+  private:
+    drh_ctx* ctx_ = nullptr;
+    uint64_t kind_ = 0;
+    hipStream_t stream_ = nullptr;
+    PoolBuf buf_;
+};
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Host wait bounded like GpuRasterizer::POLL_TIMEOUT.
+int wait_stream(hipStream_t s) {
+    hipEvent_t ev;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    e = hipEventRecord(ev, s);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(ev);
+        return hip_fail(e, "hipEventRecord");
+    }
+    auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(DRH_WAIT_TIMEOUT_S);
+    int spins = 0;
+    for (;;) {
+        e = hipEventQuery(ev);
+        if (e == hipSuccess) break;
+        if (e != hipErrorNotReady) {
+            (void)hipEventDestroy(ev);
+            return hip_fail(e, "device execution");
+        }
+        if (std::chrono::steady_clock::now() > deadline) {
+            (void)hipEventDestroy(ev);
+            return fail(DRH_ERR_TIMEOUT, "the GPU did not finish within " + std::to_string(DRH_WAIT_TIMEOUT_S) +
+                                             " s; it may be busy with another process (check rocm-smi)");
+        }
+        if (++spins > 64) std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+    (void)hipEventDestroy(ev);
+    return DRH_OK;
+}
+
+// Argument checks shared by the raster entry points, with the reference
+// binding's messages (crates/diffrast-py/src/lib.rs:162-195).
+int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float sigma) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (!(std::isfinite(sigma) && sigma > 0.0f)) return fail(DRH_ERR_INVALID_ARG, "sigma must be positive and finite");
+    if (B < 0 || T < 0 || H < 0 || W < 0) return fail(DRH_ERR_INVALID_ARG, "sizes must be non-negative");
+    if (H == 0 || W == 0) return fail(DRH_ERR_INVALID_ARG, "height and width must be non-zero");
+    if (B > 65535) return fail(DRH_ERR_TOO_LARGE, "batch of " + std::to_string(B) + " exceeds 65535 scenes per call");
+    if (H > (1 << 20) || W > (1 << 20)) return fail(DRH_ERR_TOO_LARGE, "height and width are limited to 2^20");
+    if (T > (1 << 24)) return fail(DRH_ERR_TOO_LARGE, "more than 2^24 triangles per scene");
+    if (B * T > (int64_t)INT32_MAX / 64) return fail(DRH_ERR_TOO_LARGE, "batch x triangles too large for one call");
+    return DRH_OK;
+}
+
+struct Staged {
+    Lease lease;
+    const float* dev = nullptr;
+};
+
+// Device view of an input array: the pointer itself, or a pooled copy.
+int stage_in(drh_ctx* ctx, Staged& st, uint64_t kind, const float* src, size_t n, bool host, hipStream_t s) {
+    if (n == 0) {
+        st.dev = src;
+        return DRH_OK;
+    }
+    if (!src) return fail(DRH_ERR_INVALID_ARG, "input pointer is NULL");
+    if (!host) {
+        st.dev = src;
+        return DRH_OK;
+    }
+    int rc = st.lease.acquire(ctx, kind, n * sizeof(float), s);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(st.lease.get<float>(), src, n * sizeof(float), hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+    st.dev = st.lease.get<float>();
+    return DRH_OK;
+}
+
+struct Out {
+    Lease lease;
+    float* dev = nullptr;
+    float* host_dst = nullptr;
+    size_t n = 0;
+};
+
+int stage_out(drh_ctx* ctx, Out& o, uint64_t kind, float* dst, size_t n, bool host, hipStream_t s) {
+    o.n = n;
+    if (n == 0 || !dst) {
+        o.dev = nullptr;
+        return DRH_OK;
+    }
+    if (!host) {
+        o.dev = dst;
+        return DRH_OK;
+    }
+    int rc = o.lease.acquire(ctx, kind, n * sizeof(float), s);
+    if (rc) return rc;
+    o.dev = o.lease.get<float>();
+    o.host_dst = dst;
+    return DRH_OK;
+}
+
+int copy_back(Out& o, hipStream_t s) {
+    if (!o.host_dst || o.n == 0) return DRH_OK;
+    hipError_t e = hipMemcpyAsync(o.host_dst, o.dev, o.n * sizeof(float), hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return fail(DRH_ERR_READBACK, std::string("hipMemcpyAsync D2H: ") + hipGetErrorString(e));
+    return DRH_OK;
+}
+
+int finish(uint32_t flags, hipStream_t s) {
+    if (flags & (DRH_HOST_PTRS | DRH_SYNC)) return wait_stream(s);
+    return DRH_OK;
+}
+
+// f32::powi with a runtime exponent (square-and-multiply, as the
+// compiler-builtins __powisf2 that the reference's Adam calls).
+float powi_f32(float a, int32_t b) {
+    bool recip = b < 0;
+    float r = 1.0f;
+    for (;;) {
+        if (b & 1) r *= a;
+        b /= 2;
+        if (b == 0) break;
+        a *= a;
+    }
+    return recip ? 1.0f / r : r;
+}
+
+// fit.rs:343-349
+float sigma_at(const drh_fit_config* c, int64_t i) {
+    if (c->iters <= 1) return c->sigma_end;
+    float t = (float)i / (float)(c->iters - 1);
+    return c->sigma_start * std::pow(c->sigma_end / c->sigma_start, t);
+}
+
+// The shared raster sequence: records, one raster pass, and (for the
+// gradient modes) the partial-row reduction.
+int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
+               int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
+               hipStream_t s) {
+    bool fast = !(flags & DRH_EXACT_MATH);
+    dim3 grid = drh::raster_grid(B, W, H);
+    int nblk = (int)(grid.x * grid.y);
+    Lease rec, partials, ploss;
+    int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
+    if (rc) return rc;
+    if (mode != drh::MODE_RENDER) {
+        if ((rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s))) return rc;
+        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
+    }
+    HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(), s),
+            "setup_records launch");
+    drh::RasterArgs a{};
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    a.W = W;
+    a.sigma = sigma;
+    a.rec = rec.get<float>();
+    a.bg = bgs;
+    a.target = mode == drh::MODE_LOSS ? img_in : nullptr;
+    a.grad_in = mode == drh::MODE_GRAD_IN ? img_in : nullptr;
+    a.out_img = out_img;
+    a.partials = partials.get<float>();
+    a.partial_loss = ploss.get<double>();
+    HIP_TRY(drh::launch_raster(mode, fast, a, s), "raster_kernel launch");
+    if (mode != drh::MODE_RENDER) {
+        HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3 * H * W, out_grads,
+                                   mode == drh::MODE_LOSS ? out_losses : nullptr, s),
+                "reduce_partials launch");
+    }
+    return DRH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* drh_last_error(void) { return g_err.c_str(); }
+
+int drh_params_per_triangle(void) { return NP; }
+
+int drh_create(drh_ctx** out) {
+    if (!out) return fail(DRH_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(DRH_ERR_NO_DEVICE, "no HIP device found; this build has no CPU path");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    auto* c = new drh_ctx();
+    c->device = dev;
+    c->discrete = prop.integrated == 0;
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "%s (%s, %d CUs, HIP)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    c->info = buf;
+    *out = c;
+    return DRH_OK;
+}
+
+int drh_destroy(drh_ctx* ctx) {
+    if (!ctx) return DRH_OK;
+    drh_clear_pool(ctx);
+    delete ctx;
+    return DRH_OK;
+}
+
+int drh_device_info(const drh_ctx* ctx, char* buf, size_t len) {
+    if (!ctx || !buf || len == 0) return fail(DRH_ERR_INVALID_ARG, "bad arguments");
+    std::snprintf(buf, len, "%s", ctx->info.c_str());
+    return DRH_OK;
+}
+
+int drh_is_discrete(const drh_ctx* ctx) { return ctx && ctx->discrete ? 1 : 0; }
+
+int drh_pool_stats(drh_ctx* ctx, uint64_t* hits, uint64_t* misses, uint64_t* bytes) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (hits) *hits = ctx->hits;
+    if (misses) *misses = ctx->misses;
+    if (bytes) *bytes = ctx->bytes;
+    return DRH_OK;
+}
+
+int drh_clear_pool(drh_ctx* ctx) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    DeviceGuard dg(ctx->device);
+    std::lock_guard<std::mutex> g(ctx->mu);
+    for (auto& kv : ctx->free_bufs) {
+        for (auto& b : kv.second) {
+            (void)hipEventSynchronize(b.ev);
+            (void)hipEventDestroy(b.ev);
+            (void)hipFree(b.ptr);
+        }
+    }
+    ctx->free_bufs.clear();
+    ctx->bytes = 0;
+    return DRH_OK;
+}
+
+int drh_render(drh_ctx* ctx, const float* params, const float* backgrounds, int64_t B, int64_t T, int64_t H,
+               int64_t W, float sigma, float* out_images, void* stream, uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (B == 0) return DRH_OK;
+    if (!out_images || !backgrounds) return fail(DRH_ERR_INVALID_ARG, "output or background pointer is NULL");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    bool host = flags & DRH_HOST_PTRS;
+    Staged p, bg;
+    Out img;
+    if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = run_raster(ctx, drh::MODE_RENDER, p.dev, bg.dev, nullptr, (int)B, (int)T, (int)H, (int)W, sigma,
+                         img.dev, nullptr, nullptr, flags, s)))
+        return rc;
+    if ((rc = copy_back(img, s))) return rc;
+    return finish(flags, s);
+}
+
+int drh_fused_loss_backward(drh_ctx* ctx, const float* params, const float* backgrounds, const float* targets,
+                            int64_t B, int64_t T, int64_t H, int64_t W, float sigma, float* out_losses,
+                            float* out_grads, float* out_images, void* stream, uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (B == 0) return DRH_OK;
+    if (!out_losses || !backgrounds || (T > 0 && !out_grads))
+        return fail(DRH_ERR_INVALID_ARG, "output or background pointer is NULL");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    bool host = flags & DRH_HOST_PTRS;
+    Staged p, bg, tg;
+    Out losses, grads, img;
+    if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = stage_in(ctx, tg, K_IN_IMAGES, targets, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = stage_out(ctx, losses, K_OUT_LOSSES, out_losses, (size_t)B, host, s))) return rc;
+    if ((rc = stage_out(ctx, grads, K_OUT_GRADS, out_grads, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = run_raster(ctx, drh::MODE_LOSS, p.dev, bg.dev, tg.dev, (int)B, (int)T, (int)H, (int)W, sigma, img.dev,
+                         grads.dev, losses.dev, flags, s)))
+        return rc;
+    if ((rc = copy_back(losses, s)) || (rc = copy_back(grads, s)) || (rc = copy_back(img, s))) return rc;
+    return finish(flags, s);
+}
+
+int drh_backward_from_grad(drh_ctx* ctx, const float* params, const float* backgrounds, const float* grad_images,
+                           int64_t B, int64_t T, int64_t H, int64_t W, float sigma, float* out_grads, void* stream,
+                           uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (B == 0 || T == 0) return DRH_OK;
+    if (!out_grads || !backgrounds) return fail(DRH_ERR_INVALID_ARG, "output or background pointer is NULL");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    bool host = flags & DRH_HOST_PTRS;
+    Staged p, bg, gi;
+    Out grads;
+    if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = stage_in(ctx, gi, K_IN_IMAGES, grad_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = stage_out(ctx, grads, K_OUT_GRADS, out_grads, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = run_raster(ctx, drh::MODE_GRAD_IN, p.dev, bg.dev, gi.dev, (int)B, (int)T, (int)H, (int)W, sigma,
+                         nullptr, grads.dev, nullptr, flags, s)))
+        return rc;
+    if ((rc = copy_back(grads, s))) return rc;
+    return finish(flags, s);
+}
+
+int drh_adam_project_step(drh_ctx* ctx, float* params, const float* grads, float* m, float* v, const float* lr,
+                          int64_t n, uint32_t step, float beta1, float beta2, float eps, int project, void* stream,
+                          uint32_t flags) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (n < 0 || n > INT32_MAX) return fail(DRH_ERR_INVALID_ARG, "bad parameter count");
+    if (project && n % NP != 0) return fail(DRH_ERR_INVALID_ARG, "projection needs whole triangles (n % 10 == 0)");
+    if (step == 0) return fail(DRH_ERR_INVALID_ARG, "step counts from 1");
+    if (n == 0) return DRH_OK;
+    if (!params || !grads || !m || !v || !lr) return fail(DRH_ERR_INVALID_ARG, "NULL array");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    bool host = flags & DRH_HOST_PTRS;
+    // optim.rs:309-310 bias corrections
+    float bc1 = 1.0f - powi_f32(beta1, (int32_t)step);
+    float bc2 = 1.0f - powi_f32(beta2, (int32_t)step);
+    int rc;
+    Staged g, l, pin, min_, vin;
+    if ((rc = stage_in(ctx, g, K_IN_IMAGES, grads, (size_t)n, host, s))) return rc;
+    if ((rc = stage_in(ctx, l, K_IN_BG, lr, (size_t)n, host, s))) return rc;
+    if ((rc = stage_in(ctx, pin, K_IN_PARAMS, params, (size_t)n, host, s))) return rc;
+    if ((rc = stage_in(ctx, min_, K_FIT_F32, m, (size_t)n, host, s))) return rc;
+    if ((rc = stage_in(ctx, vin, K_OUT_GRADS, v, (size_t)n, host, s))) return rc;
+    float* dp = const_cast<float*>(pin.dev);
+    float* dm = const_cast<float*>(min_.dev);
+    float* dv = const_cast<float*>(vin.dev);
+    HIP_TRY(drh::launch_adam(dp, g.dev, dm, dv, l.dev, (int)n, beta1, beta2, eps, bc1, bc2, project, s),
+            "adam_project launch");
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(params, dp, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+        HIP_TRY(hipMemcpyAsync(m, dm, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+        HIP_TRY(hipMemcpyAsync(v, dv, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+    }
+    return finish(flags, s);
+}
+
+int drh_fit_validate(const drh_fit_config* c, int64_t T) {
+    if (!c) return fail(DRH_ERR_INVALID_ARG, "config is NULL");
+    // fit.rs:98-117, in the reference's order, with its messages (fit.rs:34-44).
+    if (T <= 0) return (void)fail(DRH_ERR_INVALID_ARG, "triangles must be greater than zero"), DRH_CFG_NO_TRIANGLES;
+    if (!(std::isfinite(c->sigma_start) && std::isfinite(c->sigma_end)) || c->sigma_start <= 0.0f ||
+        c->sigma_end <= 0.0f)
+        return (void)fail(DRH_ERR_INVALID_ARG, "sigma_start and sigma_end must be positive and finite"),
+               DRH_CFG_NON_POSITIVE_SIGMA;
+    if (c->sigma_start < c->sigma_end)
+        return (void)fail(DRH_ERR_INVALID_ARG, "sigma_start must be greater than or equal to sigma_end"),
+               DRH_CFG_SIGMA_NOT_DECREASING;
+    for (float lr : {c->lr_pos, c->lr_color, c->lr_alpha})
+        if (!std::isfinite(lr) || lr <= 0.0f)
+            return (void)fail(DRH_ERR_INVALID_ARG, "learning rates must be positive and finite"),
+                   DRH_CFG_NON_POSITIVE_LEARNING_RATE;
+    return DRH_CFG_OK;
+}
+
+int drh_fit(drh_ctx* ctx, const float* target, int64_t H, int64_t W, const float* background,
+            const float* init_params, int64_t T, const drh_fit_config* cfg, float* out_losses,
+            float* out_best_params, float* out_params, drh_fit_report* report, void* stream, uint32_t flags) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (drh_fit_validate(cfg, T) != DRH_CFG_OK) return DRH_ERR_INVALID_ARG;
+    int rc = check_shape(ctx, 1, T, H, W, cfg->sigma_end);
+    if (rc) return rc;
+    if (cfg->iters < 0 || cfg->iters > INT32_MAX) return fail(DRH_ERR_INVALID_ARG, "bad iteration count");
+    if (!report || !out_best_params || (cfg->iters > 0 && !out_losses) || !background || !target || !init_params)
+        return fail(DRH_ERR_INVALID_ARG, "NULL argument");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    bool host = flags & DRH_HOST_PTRS;
+    const int n = (int)(T * NP);
+    Staged tg, bg, init;
+    if ((rc = stage_in(ctx, tg, K_IN_IMAGES, target, (size_t)H * W * 3, host, s))) return rc;
+    if ((rc = stage_in(ctx, bg, K_IN_BG, background, 3, host, s))) return rc;
+    if ((rc = stage_in(ctx, init, K_IN_PARAMS, init_params, (size_t)n, host, s))) return rc;
+
+    // Working set: params, m, v, lr, grads, best, losses, loss; one lease.
+    const size_t iters = (size_t)cfg->iters;
+    const size_t f32s = (size_t)n * 6 + iters + 1;
+    Lease work, state;
+    if ((rc = work.acquire(ctx, K_FIT_F32, f32s * sizeof(float), s))) return rc;
+    if ((rc = state.acquire(ctx, K_FIT_STATE, sizeof(drh::FitState), s))) return rc;
+    float* d_params = work.get<float>();
+    float* d_m = d_params + n;
+    float* d_v = d_m + n;
+    float* d_lr = d_v + n;
+    float* d_grads = d_lr + n;
+    float* d_best = d_grads + n;
+    float* d_losses = d_best + n;
+    float* d_loss = d_losses + iters;
+    drh::FitState* d_st = state.get<drh::FitState>();
+
+    // fit.rs:388-396 learning_rates()
+    std::vector<float> lr((size_t)n);
+    for (int64_t k = 0; k < T; k++) {
+        for (int j = 0; j < 6; j++) lr[k * NP + j] = cfg->lr_pos;
+        for (int j = 6; j < 9; j++) lr[k * NP + j] = cfg->lr_color;
+        lr[k * NP + 9] = cfg->lr_alpha;
+    }
+    drh::FitState st0{INFINITY, 0, 0, 0, -1};
+    HIP_TRY(hipMemcpyAsync(d_params, init.dev, n * sizeof(float), hipMemcpyDeviceToDevice, s), "copy init");
+    HIP_TRY(hipMemcpyAsync(d_best, init.dev, n * sizeof(float), hipMemcpyDeviceToDevice, s), "copy init");
+    HIP_TRY(hipMemsetAsync(d_m, 0, 2 * n * sizeof(float), s), "zero moments");
+    HIP_TRY(hipMemcpyAsync(d_lr, lr.data(), n * sizeof(float), hipMemcpyHostToDevice, s), "upload lr");
+    HIP_TRY(hipMemcpyAsync(d_st, &st0, sizeof st0, hipMemcpyHostToDevice, s), "upload state");
+    HIP_TRY(hipStreamSynchronize(s), "fit setup");  // lr / st0 are stack memory
+
+    const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;  // optim.rs:29-31
+    drh::FitState probe{};
+    for (int64_t i = 0; i < (int64_t)iters; i++) {
+        float sigma = sigma_at(cfg, i);
+        if ((rc = run_raster(ctx, drh::MODE_LOSS, d_params, bg.dev, tg.dev, 1, (int)T, (int)H, (int)W, sigma,
+                             nullptr, d_grads, d_loss, flags, s)))
+            return rc;
+        int32_t t = (int32_t)(i + 1);
+        float bc1 = 1.0f - powi_f32(beta1, t), bc2 = 1.0f - powi_f32(beta2, t);
+        HIP_TRY(drh::launch_fit_tail((int)i, d_loss, d_params, d_grads, d_m, d_v, d_lr, n, beta1, beta2, eps, bc1,
+                                     bc2, cfg->min_delta, cfg->patience, d_st, d_losses, d_best, s),
+                "fit_tail launch");
+        // Stop launching once the device has stopped; checked now and then
+        // rather than per step, so the loop has no per-step host round trip.
+        if ((i & 63) == 63) {
+            HIP_TRY(hipMemcpyAsync(&probe, d_st, sizeof probe, hipMemcpyDeviceToHost, s), "read state");
+            if ((rc = wait_stream(s))) return rc;
+            if (probe.stop >= 0) break;
+        }
+    }
+    drh::FitState fin{};
+    HIP_TRY(hipMemcpyAsync(&fin, d_st, sizeof fin, hipMemcpyDeviceToHost, s), "read state");
+    if ((rc = wait_stream(s))) return rc;
+    hipMemcpyKind k = host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (fin.n_losses > 0) HIP_TRY(hipMemcpyAsync(out_losses, d_losses, fin.n_losses * sizeof(float), k, s), "copy losses");
+    HIP_TRY(hipMemcpyAsync(out_best_params, d_best, n * sizeof(float), k, s), "copy best");
+    if (out_params) HIP_TRY(hipMemcpyAsync(out_params, d_params, n * sizeof(float), k, s), "copy params");
+    if ((rc = wait_stream(s))) return rc;
+    report->n_losses = fin.n_losses;
+    report->best_iter = fin.best_iter;
+    report->best_loss = fin.best_loss;
+    report->stop_reason = fin.stop < 0 ? DRH_STOP_COMPLETED : fin.stop;
+    return DRH_OK;
+}
+
+}  // extern "C"

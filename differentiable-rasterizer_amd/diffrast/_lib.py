@@ -1,0 +1,269 @@
+"""ctypes binding of libdiffrast_hip.so (the C ABI in include/diffrast_hip.h).
+
+There is no CPU fallback: if the library is missing or no HIP device is
+present, the calls raise. `Context` methods accept numpy arrays (host
+pointers, synchronous) or, via the `*_ptr` forms, raw device pointers and a
+stream handle (asynchronous), which is what the torch layer uses.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libdiffrast_hip.so"
+
+DRH_OK = 0
+ERR_NAMES = {
+    1: "NoDevice",
+    2: "Timeout",
+    3: "Device",
+    4: "Readback",
+    5: "TooLarge",
+    6: "InvalidArgument",
+}
+HOST_PTRS = 0x1
+SYNC = 0x2
+EXACT_MATH = 0x4
+
+STOP_REASONS = {0: "Completed", 1: "Converged", 2: "Diverged"}
+CONFIG_ERRORS = {1: "NoTriangles", 2: "NonPositiveSigma", 3: "SigmaNotDecreasing",
+                 4: "NonPositiveLearningRate"}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_U32 = ctypes.c_uint32
+
+
+class DiffrastError(RuntimeError):
+    """A failed C ABI call; `code` is the drh status (1-6)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERR_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+class FitConfig(ctypes.Structure):
+    _fields_ = [
+        ("iters", ctypes.c_int64),
+        ("sigma_start", ctypes.c_float),
+        ("sigma_end", ctypes.c_float),
+        ("lr_pos", ctypes.c_float),
+        ("lr_color", ctypes.c_float),
+        ("lr_alpha", ctypes.c_float),
+        ("patience", ctypes.c_int64),
+        ("min_delta", ctypes.c_float),
+    ]
+
+
+class FitReport(ctypes.Structure):
+    _fields_ = [
+        ("n_losses", ctypes.c_int64),
+        ("best_iter", ctypes.c_int64),
+        ("best_loss", ctypes.c_float),
+        ("stop_reason", ctypes.c_int32),
+    ]
+
+
+# Every symbol include/diffrast_hip.h declares, with its ctypes signature.
+SIGNATURES = {
+    "drh_create": ([ctypes.POINTER(_P)], ctypes.c_int),
+    "drh_destroy": ([_P], ctypes.c_int),
+    "drh_last_error": ([], ctypes.c_char_p),
+    "drh_device_info": ([_P, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_int),
+    "drh_is_discrete": ([_P], ctypes.c_int),
+    "drh_params_per_triangle": ([], ctypes.c_int),
+    "drh_pool_stats": ([_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                        ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "drh_clear_pool": ([_P], ctypes.c_int),
+    "drh_render": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _U32], ctypes.c_int),
+    "drh_fused_loss_backward": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _U32],
+                                ctypes.c_int),
+    "drh_backward_from_grad": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _U32], ctypes.c_int),
+    "drh_adam_project_step": ([_P, _P, _P, _P, _P, _P, _I64, _U32, _F32, _F32, _F32, ctypes.c_int, _P, _U32],
+                              ctypes.c_int),
+    "drh_fit_validate": ([ctypes.POINTER(FitConfig), _I64], ctypes.c_int),
+    "drh_fit": ([_P, _P, _I64, _I64, _P, _P, _I64, ctypes.POINTER(FitConfig), _P, _P, _P,
+                 ctypes.POINTER(FitReport), _P, _U32], ctypes.c_int),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library; raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing; build it with `python build.py` "
+                    "(or __graft_entry__.build()). There is no CPU fallback.")
+            L = ctypes.CDLL(str(LIB_PATH))
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().drh_last_error().decode(errors="replace")
+
+
+def check(rc: int) -> None:
+    if rc != DRH_OK:
+        raise DiffrastError(rc, last_error())
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _bgs(background, B: int) -> np.ndarray:
+    bg = _f32(background)
+    if bg.ndim == 1:
+        bg = np.broadcast_to(bg, (B, 3))
+    return _f32(bg.reshape(B, 3))
+
+
+class Context:
+    """A drh_ctx bound to the current HIP device (GpuRasterizer::new)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().drh_create(ctypes.byref(h)))
+        self.handle = h
+
+    def close(self) -> bool:
+        if self.handle:
+            lib().drh_destroy(self.handle)
+            self.handle = None
+            return True
+        return False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- introspection -----------------------------------------------------
+    def device_info(self) -> str:
+        buf = ctypes.create_string_buffer(512)
+        check(lib().drh_device_info(self.handle, buf, 512))
+        return buf.value.decode()
+
+    def is_discrete(self) -> bool:
+        return bool(lib().drh_is_discrete(self.handle))
+
+    def pool_stats(self) -> dict:
+        h, m, b = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().drh_pool_stats(self.handle, ctypes.byref(h), ctypes.byref(m), ctypes.byref(b)))
+        return dict(hits=h.value, misses=m.value, bytes=b.value)
+
+    def clear_pool(self) -> None:
+        check(lib().drh_clear_pool(self.handle))
+
+    # -- device-pointer forms (asynchronous on `stream`) ---------------------
+    def render_ptr(self, params, bgs, B, T, H, W, sigma, out, stream=None, flags=0):
+        check(lib().drh_render(self.handle, params, bgs, B, T, H, W, sigma, out, stream, flags))
+
+    def fused_ptr(self, params, bgs, targets, B, T, H, W, sigma, losses, grads, images=None,
+                  stream=None, flags=0):
+        check(lib().drh_fused_loss_backward(self.handle, params, bgs, targets, B, T, H, W, sigma,
+                                            losses, grads, images, stream, flags))
+
+    def from_grad_ptr(self, params, bgs, grad_images, B, T, H, W, sigma, grads, stream=None, flags=0):
+        check(lib().drh_backward_from_grad(self.handle, params, bgs, grad_images, B, T, H, W, sigma,
+                                           grads, stream, flags))
+
+    # -- host (numpy) forms, synchronous --------------------------------------
+    def render(self, params, height: int, width: int, sigma: float, background=(0, 0, 0),
+               exact: bool = False) -> np.ndarray:
+        p = _f32(params)
+        B, T = p.shape[0], p.shape[1]
+        bgs = _bgs(background, B)
+        out = np.empty((B, height, width, 3), np.float32)
+        self.render_ptr(_ptr(p), _ptr(bgs), B, T, height, width, sigma, _ptr(out),
+                        flags=HOST_PTRS | (EXACT_MATH if exact else 0))
+        return out
+
+    def fused_loss_backward(self, params, targets, sigma: float, background=(0, 0, 0),
+                            exact: bool = False, want_images: bool = False):
+        p, t = _f32(params), _f32(targets)
+        B, T = p.shape[0], p.shape[1]
+        H, W = t.shape[1], t.shape[2]
+        bgs = _bgs(background, B)
+        losses = np.empty(B, np.float32)
+        grads = np.empty((B, T, 10), np.float32)
+        imgs = np.empty((B, H, W, 3), np.float32) if want_images else None
+        self.fused_ptr(_ptr(p), _ptr(bgs), _ptr(t), B, T, H, W, sigma, _ptr(losses), _ptr(grads),
+                       _ptr(imgs), flags=HOST_PTRS | (EXACT_MATH if exact else 0))
+        return (losses, grads, imgs) if want_images else (losses, grads)
+
+    def backward_from_grad(self, params, grad_images, sigma: float, background=(0, 0, 0),
+                           exact: bool = False) -> np.ndarray:
+        p, g = _f32(params), _f32(grad_images)
+        B, T = p.shape[0], p.shape[1]
+        H, W = g.shape[1], g.shape[2]
+        bgs = _bgs(background, B)
+        grads = np.zeros((B, T, 10), np.float32)
+        self.from_grad_ptr(_ptr(p), _ptr(bgs), _ptr(g), B, T, H, W, sigma, _ptr(grads),
+                           flags=HOST_PTRS | (EXACT_MATH if exact else 0))
+        return grads
+
+    def adam_project_step(self, params: np.ndarray, grads, m: np.ndarray, v: np.ndarray, lr,
+                          step: int, beta1=0.9, beta2=0.999, eps=1e-8, project=True) -> None:
+        """In place on params, m, v (float32 contiguous numpy arrays)."""
+        g, l = _f32(grads), _f32(lr)
+        for a in (params, m, v):
+            assert a.dtype == np.float32 and a.flags.c_contiguous
+        check(lib().drh_adam_project_step(self.handle, _ptr(params), _ptr(g), _ptr(m), _ptr(v), _ptr(l),
+                                          params.size, step, beta1, beta2, eps, int(project), None,
+                                          HOST_PTRS))
+
+    def fit(self, target, init_params, background, iters=1500, sigma_start=0.02, sigma_end=0.0015,
+            lr_pos=0.004, lr_color=0.02, lr_alpha=0.01, patience=250, min_delta=1e-7):
+        """fit.rs:166-288 on the device from a given initial scene."""
+        t = _f32(target)
+        H, W = t.shape[0], t.shape[1]
+        p = _f32(init_params).reshape(-1, 10)
+        T = p.shape[0]
+        bg = _f32(background).reshape(3)
+        cfg = FitConfig(iters, sigma_start, sigma_end, lr_pos, lr_color, lr_alpha,
+                        -1 if patience is None else int(patience), min_delta)
+        losses = np.empty(max(iters, 1), np.float32)
+        best = np.empty_like(p)
+        last = np.empty_like(p)
+        rep = FitReport()
+        check(lib().drh_fit(self.handle, _ptr(t), H, W, _ptr(bg), _ptr(p), T, ctypes.byref(cfg),
+                            _ptr(losses), _ptr(best), _ptr(last), ctypes.byref(rep), None, HOST_PTRS))
+        return dict(losses=losses[: rep.n_losses].copy(), best_params=best, params=last,
+                    best_iter=int(rep.best_iter), best_loss=float(rep.best_loss),
+                    stop_reason=STOP_REASONS[rep.stop_reason])
+
+
+def validate_fit_config(T: int, **cfg) -> str | None:
+    """FitConfig::validate (fit.rs:98-117): None when valid, else the error name."""
+    c = dict(iters=1500, sigma_start=0.02, sigma_end=0.0015, lr_pos=0.004, lr_color=0.02,
+             lr_alpha=0.01, patience=250, min_delta=1e-7)
+    c.update(cfg)
+    conf = FitConfig(c["iters"], c["sigma_start"], c["sigma_end"], c["lr_pos"], c["lr_color"],
+                     c["lr_alpha"], -1 if c["patience"] is None else c["patience"], c["min_delta"])
+    rc = lib().drh_fit_validate(ctypes.byref(conf), T)
+    return CONFIG_ERRORS.get(rc)
+
+
+def params_per_triangle() -> int:
+    return int(lib().drh_params_per_triangle())

@@ -1,0 +1,161 @@
+/*
+ * diffrast_hip — C ABI of the MI355X (gfx950) soft-triangle rasterizer.
+ *
+ * Plain pointers and sizes only. Every function returns a status code; the
+ * message for the last failure on the calling thread is drh_last_error().
+ *
+ * Layouts are the reference's (crates/diffrast-py/src/lib.rs:10-13):
+ *   params      B x T x 10 float, [x0,y0,x1,y1,x2,y2,r,g,b,a] per triangle,
+ *               vertices in normalized image space, index 0 drawn first
+ *   images      B x H x W x 3 float, linear RGB, row-major
+ *   backgrounds B x 3 float (per scene, as the GPU crate packs them,
+ *               crates/diffrast-gpu/src/lib.rs:936-954)
+ *
+ * Pointers are device pointers unless DRH_HOST_PTRS is set. With device
+ * pointers a call only enqueues work on `stream` (a hipStream_t; NULL is the
+ * null stream) and returns; with host pointers it stages through pooled device
+ * buffers and returns once the results are back on the host.
+ *
+ * A context is safe to use from several threads at once: scratch buffers come
+ * from a locked pool and a buffer reused on another stream waits for the work
+ * that last used it.
+ */
+#ifndef DIFFRAST_HIP_H
+#define DIFFRAST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. 1-5 are the reference's GpuError variants
+ * (crates/diffrast-gpu/src/lib.rs:42-50); 6 covers the argument checks its
+ * Python binding raises ValueError for (crates/diffrast-py/src/lib.rs:85-94,
+ * 162-167, 185-195, 261-273). */
+enum {
+    DRH_OK = 0,
+    DRH_ERR_NO_DEVICE = 1,   /* GpuError::NoAdapter */
+    DRH_ERR_TIMEOUT = 2,     /* GpuError::Timeout: a host wait exceeded DRH_WAIT_TIMEOUT_S */
+    DRH_ERR_DEVICE = 3,      /* GpuError::DeviceRequest: a HIP runtime failure */
+    DRH_ERR_READBACK = 4,    /* GpuError::Readback: copying results to the host failed */
+    DRH_ERR_TOO_LARGE = 5,   /* GpuError::TooLarge: sizes beyond what one call supports */
+    DRH_ERR_INVALID_ARG = 6  /* bad sigma, zero height/width, NULL pointer, bad config */
+};
+
+/* Flags. */
+#define DRH_HOST_PTRS 0x1u  /* array arguments are host memory */
+#define DRH_SYNC 0x2u       /* with device pointers: wait for the stream before returning */
+#define DRH_EXACT_MATH 0x4u /* IEEE division, sqrt and expf in the per-pixel geometry */
+
+/* Bounded host wait, as GpuRasterizer::POLL_TIMEOUT (crates/diffrast-gpu/src/lib.rs:229). */
+#define DRH_WAIT_TIMEOUT_S 60
+
+typedef struct drh_ctx drh_ctx;
+
+/* GpuRasterizer::new (crates/diffrast-gpu/src/lib.rs:238-319): binds the
+ * current HIP device. DRH_ERR_NO_DEVICE when there is none. */
+int drh_create(drh_ctx **out);
+
+/* shutdown_gpu (crates/diffrast-py/src/lib.rs:435-444): frees the pool and
+ * the context. NULL is accepted. */
+int drh_destroy(drh_ctx *ctx);
+
+/* Message for the last failure on this thread ("" when none). */
+const char *drh_last_error(void);
+
+/* adapter_info (crates/diffrast-gpu/src/lib.rs:370-373). */
+int drh_device_info(const drh_ctx *ctx, char *buf, size_t len);
+
+/* is_discrete (crates/diffrast-gpu/src/lib.rs:383-385): 1 or 0. */
+int drh_is_discrete(const drh_ctx *ctx);
+
+/* params_per_triangle (crates/diffrast-py/src/lib.rs:452-456): 10. */
+int drh_params_per_triangle(void);
+
+/* pool_stats / clear_pool (crates/diffrast-gpu/src/lib.rs:345-356). */
+int drh_pool_stats(drh_ctx *ctx, uint64_t *hits, uint64_t *misses, uint64_t *bytes);
+int drh_clear_pool(drh_ctx *ctx);
+
+/* Batched forward render: render_many (crates/diffrast-gpu/src/lib.rs:615-633)
+ * and render_batch (crates/diffrast-py/src/lib.rs:174-231), per-pixel
+ * semantics of raster.rs:37-168. out_images is B x H x W x 3. B == 0 is a
+ * no-op; T == 0 renders the backgrounds. */
+int drh_render(drh_ctx *ctx, const float *params, const float *backgrounds, int64_t B, int64_t T,
+               int64_t H, int64_t W, float sigma, float *out_images, void *stream, uint32_t flags);
+
+/* Render, per-item MSE and its parameter gradients in one call:
+ * backward_many (crates/diffrast-gpu/src/lib.rs:639-646) and
+ * fused_loss_backward (crates/diffrast-py/src/lib.rs:333-412), semantics of
+ * grad.rs:56-182 and canvas.rs:45-58. out_losses is B floats, out_grads
+ * B x T x 10. out_images (B x H x W x 3) may be NULL. */
+int drh_fused_loss_backward(drh_ctx *ctx, const float *params, const float *backgrounds,
+                            const float *targets, int64_t B, int64_t T, int64_t H, int64_t W,
+                            float sigma, float *out_losses, float *out_grads, float *out_images,
+                            void *stream, uint32_t flags);
+
+/* Parameter gradients from an upstream image gradient dL/dpixel
+ * (B x H x W x 3): backward_many_from_grad
+ * (crates/diffrast-gpu/src/lib.rs:828-910) and backward_batch
+ * (crates/diffrast-py/src/lib.rs:245-324). out_grads is B x T x 10. */
+int drh_backward_from_grad(drh_ctx *ctx, const float *params, const float *backgrounds,
+                           const float *grad_images, int64_t B, int64_t T, int64_t H, int64_t W,
+                           float sigma, float *out_grads, void *stream, uint32_t flags);
+
+/* One Adam step (optim.rs:40-60) over n parameters with per-parameter
+ * learning rates, then fit.rs:399-424 project() when `project` is nonzero
+ * (n must then be a multiple of 10). `step` is the step count after the
+ * increment (the reference's `t`, starting at 1). */
+int drh_adam_project_step(drh_ctx *ctx, float *params, const float *grads, float *m, float *v,
+                          const float *lr, int64_t n, uint32_t step, float beta1, float beta2,
+                          float eps, int project, void *stream, uint32_t flags);
+
+/* FitConfig (crates/diffrast/src/fit.rs:49-65) minus the scene size and seed,
+ * which drh_fit takes as the initial scene. patience < 0 means None. */
+typedef struct {
+    int64_t iters;
+    float sigma_start, sigma_end;
+    float lr_pos, lr_color, lr_alpha;
+    int64_t patience;
+    float min_delta;
+} drh_fit_config;
+
+/* StopReason (fit.rs:14-23). */
+enum { DRH_STOP_COMPLETED = 0, DRH_STOP_CONVERGED = 1, DRH_STOP_DIVERGED = 2 };
+
+/* ConfigError (fit.rs:26-32) as returned by drh_fit_validate; 0 when valid. */
+enum {
+    DRH_CFG_OK = 0,
+    DRH_CFG_NO_TRIANGLES = 1,
+    DRH_CFG_NON_POSITIVE_SIGMA = 2,
+    DRH_CFG_SIGMA_NOT_DECREASING = 3,
+    DRH_CFG_NON_POSITIVE_LEARNING_RATE = 4
+};
+
+/* FitReport (fit.rs:128-140) minus the scene, which drh_fit writes out. */
+typedef struct {
+    int64_t n_losses;
+    int64_t best_iter;
+    float best_loss;
+    int32_t stop_reason;
+} drh_fit_report;
+
+/* FitConfig::validate (fit.rs:98-117) for a scene of T triangles. */
+int drh_fit_validate(const drh_fit_config *cfg, int64_t T);
+
+/* The fit loop (fit.rs:166-288) from a given initial scene, with every step
+ * on the device: sigma annealing, fused loss and gradients, divergence, best
+ * snapshot and patience bookkeeping, Adam and projection. The loss is read
+ * back once at the end, not per step. target is H x W x 3, init_params and
+ * out_best_params T x 10, out_losses room for cfg->iters floats,
+ * out_params (optional) receives the last iterate. */
+int drh_fit(drh_ctx *ctx, const float *target, int64_t H, int64_t W, const float *background,
+            const float *init_params, int64_t T, const drh_fit_config *cfg, float *out_losses,
+            float *out_best_params, float *out_params, drh_fit_report *report, void *stream,
+            uint32_t flags);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DIFFRAST_HIP_H */
