@@ -69,6 +69,14 @@ struct PoolBuf {
 
 }  // namespace
 
+namespace {
+enum TimedKernel : int { TK_SETUP = 0, TK_RASTER, TK_REDUCE, TK_ADAM, TK_COUNT };
+struct TimedLaunch {
+    int kernel;
+    hipEvent_t start, stop;
+};
+}  // namespace
+
 struct drh_ctx {
     int device = 0;
     bool discrete = true;
@@ -76,6 +84,9 @@ struct drh_ctx {
     std::mutex mu;
     std::unordered_map<uint64_t, std::vector<PoolBuf>> free_bufs;
     uint64_t hits = 0, misses = 0, bytes = 0;
+    // kernel timing (drh_timing_enable / drh_timing_read)
+    bool timing = false;
+    std::vector<TimedLaunch> pending;
 };
 
 namespace {
@@ -302,6 +313,29 @@ float sigma_at(const drh_fit_config* c, int64_t i) {
     return c->sigma_start * std::pow(c->sigma_end / c->sigma_start, t);
 }
 
+// Brackets one kernel launch with events when the context is timing.
+class KernelTimer {
+  public:
+    KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s) : ctx_(ctx), s_(s) {
+        if (!ctx->timing) return;
+        l_.kernel = kernel;
+        if (hipEventCreate(&l_.start) != hipSuccess || hipEventCreate(&l_.stop) != hipSuccess) return;
+        on_ = hipEventRecord(l_.start, s) == hipSuccess;
+    }
+    ~KernelTimer() {
+        if (!on_) return;
+        (void)hipEventRecord(l_.stop, s_);
+        std::lock_guard<std::mutex> g(ctx_->mu);
+        ctx_->pending.push_back(l_);
+    }
+
+  private:
+    drh_ctx* ctx_;
+    hipStream_t s_;
+    TimedLaunch l_{};
+    bool on_ = false;
+};
+
 // The shared raster sequence: records, one raster pass, and (for the
 // gradient modes) the partial-row reduction.
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
@@ -317,8 +351,11 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         if ((rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s))) return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
     }
-    HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(), s),
-            "setup_records launch");
+    {
+        KernelTimer kt(ctx, TK_SETUP, s);
+        HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(), s),
+                "setup_records launch");
+    }
     drh::RasterArgs a{};
     a.B = B;
     a.T = T;
@@ -332,8 +369,12 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.out_img = out_img;
     a.partials = partials.get<float>();
     a.partial_loss = ploss.get<double>();
-    HIP_TRY(drh::launch_raster(mode, fast, a, s), "raster_kernel launch");
+    {
+        KernelTimer kt(ctx, TK_RASTER, s);
+        HIP_TRY(drh::launch_raster(mode, fast, a, s), "raster_kernel launch");
+    }
     if (mode != drh::MODE_RENDER) {
+        KernelTimer kt(ctx, TK_REDUCE, s);
         HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3 * H * W, out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s),
                 "reduce_partials launch");
@@ -407,6 +448,46 @@ int drh_clear_pool(drh_ctx* ctx) {
     ctx->free_bufs.clear();
     ctx->bytes = 0;
     return DRH_OK;
+}
+
+int drh_timing_enable(drh_ctx* ctx, int enable) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->timing = enable != 0;
+    return DRH_OK;
+}
+
+int drh_timing_read(drh_ctx* ctx, drh_timings* out) {
+    if (!ctx || !out) return fail(DRH_ERR_INVALID_ARG, "bad arguments");
+    std::vector<TimedLaunch> launches;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        launches.swap(ctx->pending);
+    }
+    double ms[TK_COUNT] = {0, 0, 0, 0};
+    int64_t n[TK_COUNT] = {0, 0, 0, 0};
+    int rc = DRH_OK;
+    for (auto& l : launches) {
+        float t = 0.0f;
+        if (rc == DRH_OK) {
+            hipError_t e = hipEventSynchronize(l.stop);
+            if (e == hipSuccess) e = hipEventElapsedTime(&t, l.start, l.stop);
+            if (e != hipSuccess) rc = hip_fail(e, "kernel timing");
+        }
+        ms[l.kernel] += t;
+        n[l.kernel] += 1;
+        (void)hipEventDestroy(l.start);
+        (void)hipEventDestroy(l.stop);
+    }
+    out->setup_ms = ms[TK_SETUP];
+    out->raster_ms = ms[TK_RASTER];
+    out->reduce_ms = ms[TK_REDUCE];
+    out->adam_ms = ms[TK_ADAM];
+    out->setup_n = n[TK_SETUP];
+    out->raster_n = n[TK_RASTER];
+    out->reduce_n = n[TK_REDUCE];
+    out->adam_n = n[TK_ADAM];
+    return rc;
 }
 
 int drh_render(drh_ctx* ctx, const float* params, const float* backgrounds, int64_t B, int64_t T, int64_t H,
@@ -504,8 +585,11 @@ int drh_adam_project_step(drh_ctx* ctx, float* params, const float* grads, float
     float* dp = const_cast<float*>(pin.dev);
     float* dm = const_cast<float*>(min_.dev);
     float* dv = const_cast<float*>(vin.dev);
-    HIP_TRY(drh::launch_adam(dp, g.dev, dm, dv, l.dev, (int)n, beta1, beta2, eps, bc1, bc2, project, s),
-            "adam_project launch");
+    {
+        KernelTimer kt(ctx, TK_ADAM, s);
+        HIP_TRY(drh::launch_adam(dp, g.dev, dm, dv, l.dev, (int)n, beta1, beta2, eps, bc1, bc2, project, s),
+                "adam_project launch");
+    }
     if (host) {
         HIP_TRY(hipMemcpyAsync(params, dp, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
         HIP_TRY(hipMemcpyAsync(m, dm, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
@@ -591,9 +675,12 @@ int drh_fit(drh_ctx* ctx, const float* target, int64_t H, int64_t W, const float
             return rc;
         int32_t t = (int32_t)(i + 1);
         float bc1 = 1.0f - powi_f32(beta1, t), bc2 = 1.0f - powi_f32(beta2, t);
-        HIP_TRY(drh::launch_fit_tail((int)i, d_loss, d_params, d_grads, d_m, d_v, d_lr, n, beta1, beta2, eps, bc1,
-                                     bc2, cfg->min_delta, cfg->patience, d_st, d_losses, d_best, s),
-                "fit_tail launch");
+        {
+            KernelTimer kt(ctx, TK_ADAM, s);
+            HIP_TRY(drh::launch_fit_tail((int)i, d_loss, d_params, d_grads, d_m, d_v, d_lr, n, beta1, beta2, eps,
+                                         bc1, bc2, cfg->min_delta, cfg->patience, d_st, d_losses, d_best, s),
+                    "fit_tail launch");
+        }
         // Stop launching once the device has stopped; checked now and then
         // rather than per step, so the loop has no per-step host round trip.
         if ((i & 63) == 63) {

@@ -69,8 +69,23 @@ class FitReport(ctypes.Structure):
     ]
 
 
+class Timings(ctypes.Structure):
+    _fields_ = [
+        ("setup_ms", ctypes.c_double),
+        ("raster_ms", ctypes.c_double),
+        ("reduce_ms", ctypes.c_double),
+        ("adam_ms", ctypes.c_double),
+        ("setup_n", ctypes.c_int64),
+        ("raster_n", ctypes.c_int64),
+        ("reduce_n", ctypes.c_int64),
+        ("adam_n", ctypes.c_int64),
+    ]
+
+
 # Every symbol include/diffrast_hip.h declares, with its ctypes signature.
 SIGNATURES = {
+    "drh_timing_enable": ([_P, ctypes.c_int], ctypes.c_int),
+    "drh_timing_read": ([_P, ctypes.POINTER(Timings)], ctypes.c_int),
     "drh_create": ([ctypes.POINTER(_P)], ctypes.c_int),
     "drh_destroy": ([_P], ctypes.c_int),
     "drh_last_error": ([], ctypes.c_char_p),
@@ -174,6 +189,16 @@ class Context:
 
     def clear_pool(self) -> None:
         check(lib().drh_clear_pool(self.handle))
+
+    def timing(self, enable: bool) -> None:
+        """Bracket every launched kernel with HIP events (BackwardTimings)."""
+        check(lib().drh_timing_enable(self.handle, int(enable)))
+
+    def read_timings(self) -> dict:
+        """Accumulated kernel milliseconds and launch counts since the last read."""
+        t = Timings()
+        check(lib().drh_timing_read(self.handle, ctypes.byref(t)))
+        return {name: getattr(t, name) for name, _ in Timings._fields_}
 
     # -- device-pointer forms (asynchronous on `stream`) ---------------------
     def render_ptr(self, params, bgs, B, T, H, W, sigma, out, stream=None, flags=0):

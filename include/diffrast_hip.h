@@ -78,6 +78,20 @@ int drh_params_per_triangle(void);
 int drh_pool_stats(drh_ctx *ctx, uint64_t *hits, uint64_t *misses, uint64_t *bytes);
 int drh_clear_pool(drh_ctx *ctx);
 
+/* Device-side kernel timings, the counterpart of BackwardTimings /
+ * backward_many_timed (crates/diffrast-gpu/src/lib.rs:96-114, 649-655). While
+ * enabled, every kernel a call launches is bracketed by HIP events on the
+ * call's stream; drh_timing_read waits for them, returns the accumulated
+ * milliseconds and launch counts since the last read, and resets them. The
+ * events do not synchronize the host between kernels. */
+typedef struct {
+    double setup_ms, raster_ms, reduce_ms, adam_ms;
+    int64_t setup_n, raster_n, reduce_n, adam_n;
+} drh_timings;
+
+int drh_timing_enable(drh_ctx *ctx, int enable);
+int drh_timing_read(drh_ctx *ctx, drh_timings *out);
+
 /* Batched forward render: render_many (crates/diffrast-gpu/src/lib.rs:615-633)
  * and render_batch (crates/diffrast-py/src/lib.rs:174-231), per-pixel
  * semantics of raster.rs:37-168. out_images is B x H x W x 3. B == 0 is a
