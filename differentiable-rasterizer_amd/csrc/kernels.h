@@ -12,7 +12,7 @@ constexpr int WAVES = 4;  // waves per block: 2x2 tiles, a 16x16 pixel region
 constexpr int CH = 128;   // triangles per chunk (LDS accumulators are per chunk)
 
 // Per-triangle record, REC floats, written by setup_records.
-constexpr int REC = 48;
+constexpr int REC = 40;
 enum RecField : int {
     R_V = 0,       // 6: vertices x0 y0 x1 y1 x2 y2
     R_C = 6,       // 3: colour

@@ -138,14 +138,36 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
     for (int j = 0; j < 3; j++) r[R_RLEN2 + j] = rlen2[j];
     for (int j = 0; j < 6; j++) r[R_N + j] = n[j];
     for (int j = 0; j < 3; j++) r[R_OFF + j] = off[j];
-    // far outside: true distance > 20 sigma  =>  w <= alpha * sigmoid(-19.99) < MIN_WEIGHT
-    // deep inside: distance to the edge > 18 sigma  =>  sigmoid rounds to exactly 1.0f
-    r[R_FAR] = 20.0f * sig + slack;
-    r[R_DEEP] = -(18.0f * sig + slack);
+    // Far outside: at a true distance d >= sigma (ln(alpha / MIN_WEIGHT) + 0.05)
+    // the weight is alpha * sigmoid(-d / sigma) < alpha e^(-d / sigma)
+    // <= 0.951 MIN_WEIGHT, which the f32 rounding of the reference's sigmoid
+    // and product (a few ulp) cannot lift to MIN_WEIGHT: it skips the pair too.
+    // Deep inside: at a distance to the edge above 17 sigma, exp(-x) < 4.2e-8
+    // < 2^-24, so the reference's 1 / (1 + exp(-x)) rounds to exactly 1.0f.
+    float xfar = fmaxf(logf(alpha * (1.0f / MIN_WEIGHT)) + 0.05f, 0.0f);
+    r[R_FAR] = (xfar == xfar ? xfar : 0.0f) * sig + slack;
+    r[R_DEEP] = -(17.0f * sig + slack);
     for (int j = R_DEEP + 1; j < REC; j++) r[j] = 0.0f;
 }
 
 // ---------------------------------------------------------------- per-pair math
+
+// One triangle record held in registers. The three vector loads (16 + 16 + 8 floats)
+// of a wave-uniform address become s_load_dwordx16/x16/x8 issued together, so a list
+// entry costs one scalar-memory round trip instead of one per field.
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f8v __attribute__((ext_vector_type(8)));
+static_assert(REC == 40, "load_rec reads 16 + 16 + 8 floats");
+struct Rec {
+    f16v a, b;
+    f8v c;
+    __device__ float f(int i) const { return i < 16 ? a[i] : (i < 32 ? b[i - 16] : c[i - 32]); }
+    __device__ int i(int k) const { return __float_as_int(f(k)); }
+};
+__device__ inline Rec load_rec(const float* __restrict__ r) {
+    const f16v* v = reinterpret_cast<const f16v*>(r);
+    return Rec{v[0], v[1], *reinterpret_cast<const f8v*>(r + 32)};
+}
 
 struct Pix {
     float px, py;
@@ -169,9 +191,10 @@ __device__ inline float sigmoid_f(float x) {
 // grad.rs:235-247. The cross products, the inside test and the nearest-point
 // arithmetic round exactly as the reference does (no FMA), because near an
 // edge an error of 1e-7 in position is magnified by 1/sigma in the coverage.
-// With `fast` (a triangle of moderate coordinates in a FAST build) the
-// projection quotient comes from a refined reciprocal and the square root from
-// the hardware instruction; otherwise both are IEEE operations.
+// QUICK (a triangle of moderate coordinates in a fast-math build) forms the
+// projection quotient from a refined reciprocal and takes the hardware square
+// root; otherwise both are IEEE operations. The choice is made per triangle,
+// outside this function, by a wave-uniform branch.
 struct Geo {
     float sd;      // signed distance, positive inside
     float dist;    // |nearest segment distance|
@@ -181,14 +204,26 @@ struct Geo {
     int edge;      // nearest edge index, first minimum wins (grad.rs:236-242)
 };
 
-__device__ inline Geo geometry(const float* __restrict__ r, Pix p, bool fast) {
+// The reference compares square-rooted distances (grad.rs:236-242): an earlier
+// edge whose d2 is an ulp or two above the minimum can round to the same
+// distance and then wins. That is routine for the overlapping edges of a
+// collinear triangle. Kept out of line of the common path: the empty volatile
+// asm stops the compiler from speculating the IEEE square roots into every
+// evaluation.
+__device__ inline bool same_sqrt(float a, float b) {
+    asm volatile("");
+    return sqrtf(a) == sqrtf(b);
+}
+
+template <bool QUICK>
+__device__ inline Geo geometry(const Rec& r, Pix p) {
     float apx[3], apy[3];
     for (int j = 0; j < 3; j++) {
-        apx[j] = p.px - r[R_V + 2 * j];
-        apy[j] = p.py - r[R_V + 2 * j + 1];
+        apx[j] = p.px - r.f(R_V + 2 * j);
+        apy[j] = p.py - r.f(R_V + 2 * j + 1);
     }
     float c[3];
-    for (int j = 0; j < 3; j++) c[j] = r[R_E + 2 * j] * apy[j] - r[R_E + 2 * j + 1] * apx[j];
+    for (int j = 0; j < 3; j++) c[j] = r.f(R_E + 2 * j) * apy[j] - r.f(R_E + 2 * j + 1) * apx[j];
     bool inside = (c[0] >= 0.0f && c[1] >= 0.0f && c[2] >= 0.0f) ||
                   (c[0] <= 0.0f && c[1] <= 0.0f && c[2] <= 0.0f);
     Geo g;
@@ -197,22 +232,22 @@ __device__ inline Geo geometry(const float* __restrict__ r, Pix p, bool fast) {
     g.edge = 0;
     g.t = 0.0f;
     for (int j = 0; j < 3; j++) {
-        float ex = r[R_E + 2 * j], ey = r[R_E + 2 * j + 1];
+        float ex = r.f(R_E + 2 * j), ey = r.f(R_E + 2 * j + 1);
         float dot = apx[j] * ex + apy[j] * ey;
         float t;
-        if (fast) {
+        if (QUICK) {
             // dot / len2 as the reference rounds it: with rlen2 the correctly
             // rounded 1/len2, one residual step q0 + (dot - q0*len2)*rlen2
             // gives the correctly rounded quotient (Markstein). The nearest
             // point then matches the reference bit for bit; an ulp off in t
             // moves the distance of an on-edge pixel by ~|e|*6e-8, which 1/sigma
             // magnifies into visible coverage error at small sigma.
-            float rl = r[R_RLEN2 + j];
+            float rl = r.f(R_RLEN2 + j);
             float q0 = dot * rl;
-            float res = fmaf(-q0, r[R_LEN2 + j], dot);
+            float res = fmaf(-q0, r.f(R_LEN2 + j), dot);
             t = __builtin_amdgcn_fmed3f(fmaf(res, rl, q0), 0.0f, 1.0f);
         } else {
-            float len2 = r[R_LEN2 + j];
+            float len2 = r.f(R_LEN2 + j);
             t = (len2 <= 1e-20f) ? 0.0f : rust_clamp(dot / len2, 0.0f, 1.0f);
         }
         float dx = apx[j] - t * ex;
@@ -226,47 +261,108 @@ __device__ inline Geo geometry(const float* __restrict__ r, Pix p, bool fast) {
             g.t = t;
         }
     }
-    // The reference compares the square-rooted distances (grad.rs:236-242):
-    // an earlier edge whose d2 is an ulp or two above the minimum can round to
-    // the same distance and then wins. That is routine for overlapping edges
-    // of a collinear triangle, so such near ties are re-checked with the
-    // correctly rounded sqrt the reference uses.
-    for (int j = 0; j < 2; j++) {
-        if (j < g.edge && d2v[j] <= best * 1.0000005f && sqrtf(d2v[j]) == sqrtf(best)) {
-            g.edge = j;
-            g.t = tv[j];
-            break;
+    const float near = best * 1.0000005f;
+    if ((g.edge > 0 && d2v[0] <= near) || (g.edge > 1 && d2v[1] <= near)) {
+        for (int j = 0; j < 2; j++) {
+            if (j < g.edge && d2v[j] <= near && same_sqrt(d2v[j], best)) {
+                g.edge = j;
+                g.t = tv[j];
+                break;
+            }
         }
     }
     // selects rather than a lane-varying index into the (scalar) record
     const int ed = g.edge;
-    g.ax = ed == 0 ? r[R_V + 0] : (ed == 1 ? r[R_V + 2] : r[R_V + 4]);
-    g.ay = ed == 0 ? r[R_V + 1] : (ed == 1 ? r[R_V + 3] : r[R_V + 5]);
-    g.ex = ed == 0 ? r[R_E + 0] : (ed == 1 ? r[R_E + 2] : r[R_E + 4]);
-    g.ey = ed == 0 ? r[R_E + 1] : (ed == 1 ? r[R_E + 3] : r[R_E + 5]);
+    g.ax = ed == 0 ? r.f(R_V + 0) : (ed == 1 ? r.f(R_V + 2) : r.f(R_V + 4));
+    g.ay = ed == 0 ? r.f(R_V + 1) : (ed == 1 ? r.f(R_V + 3) : r.f(R_V + 5));
+    g.ex = ed == 0 ? r.f(R_E + 0) : (ed == 1 ? r.f(R_E + 2) : r.f(R_E + 4));
+    g.ey = ed == 0 ? r.f(R_E + 1) : (ed == 1 ? r.f(R_E + 3) : r.f(R_E + 5));
     // sqrt is monotone, so sqrt(min d2) == min sqrt(d2) (raster.rs:97-99).
-    g.dist = fast ? __builtin_amdgcn_sqrtf(best) : sqrtf(best);
+    g.dist = QUICK ? __builtin_amdgcn_sqrtf(best) : sqrtf(best);
     g.sd = inside ? g.dist : -g.dist;
     return g;
 }
 
-// ---------------------------------------------------------------- wave reduction
+// Exact-path coverage of one pair. The branch on the triangle's F_FAST flag is
+// wave-uniform; the empty volatile asm keeps the compiler from if-converting
+// it, which would evaluate both quotient and square-root variants every time.
+template <bool FAST>
+__device__ inline void exact_cov(const Rec& r, Pix p, float rsig, float sig, Geo& g, float& cov) {
+    if (FAST && (r.i(R_FLAGS) & F_FAST)) {
+        g = geometry<true>(r, p);
+    } else {
+        asm volatile("");
+        g = geometry<false>(r, p);
+    }
+    cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
+}
 
-// Full wave64 sum, valid in lane 63: xor1, xor2 (quad_perm), half-row and row
-// mirrors give every lane its row sum; row_bcast15 / row_bcast31 fold the rows.
-template <int ctrl, int rmask>
-__device__ inline float dpp_add(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xF, false));
+// ---------------------------------------------------------------- wave reductions
+
+// DPP controls (gfx9 encoding) used below; every source lane is inside the row.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_ROR8 = 0x128;    // row_ror:8, i.e. lane ^ 8 within a row of 16
+constexpr int DPP_HALF_MIRROR = 0x141; // lane -> 7 - lane within each half row of 8
+
+template <int ctrl>
+__device__ inline float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
 }
-__device__ inline float wave_sum_to_lane63(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
-    v = dpp_add<0x140, 0xF>(v);  // row_mirror
-    v = dpp_add<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
-    v = dpp_add<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
-    return v;
+
+// v_permlane32_swap exchanges the upper half of x with the lower half of y, so
+// the sum gives lanes 0-31 x[l] + x[l+32] and lanes 32-63 y[l-32] + y[l].
+__device__ inline float fold32(float x, float y) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// v_permlane16_swap exchanges the odd rows of x with the even rows of y: rows
+// 0 and 2 get the row-pair sums of x, rows 1 and 3 those of y.
+__device__ inline float fold16(float x, float y) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Transposed wave64 sum of ten per-lane values. Each folding step halves the
+// lanes a value is spread over while the values share the registers, so the
+// whole reduction is 26 VALU instructions instead of 60 for ten independent
+// trees. The sum of a[p] ends in lane red10_lane(p).
+__device__ inline float wave_reduce10(const float (&a)[NP], int lane) {
+    float b0 = fold32(a[0], a[5]), b1 = fold32(a[1], a[6]), b2 = fold32(a[2], a[7]);
+    float b3 = fold32(a[3], a[8]), b4 = fold32(a[4], a[9]);
+    float c0 = fold16(b0, b1);    // rows hold a0 a1 a5 a6
+    float c1 = fold16(b2, b3);    // rows hold a2 a3 a7 a8
+    float c2 = fold16(b4, 0.0f);  // rows hold a4 -  a9 -
+    const bool h8 = (lane & 8) != 0, h4 = (lane & 4) != 0;
+    float d0 = (h8 ? c1 : c0) + dpp<DPP_ROW_ROR8>(h8 ? c0 : c1);
+    float d1 = c2 + dpp<DPP_ROW_ROR8>(c2);
+    float e = (h4 ? d1 : d0) + dpp<DPP_HALF_MIRROR>(h4 ? d0 : d1);
+    e += dpp<DPP_XOR2>(e);
+    e += dpp<DPP_XOR1>(e);
+    return e;
+}
+// Parameter whose total wave_reduce10 leaves in `lane`, or -1.
+__device__ inline int red10_param(int lane) {
+    const int row = lane >> 4, g = lane & 15;
+    if (g == 0) return row == 0 ? 0 : row == 1 ? 1 : row == 2 ? 5 : 6;
+    if (g == 8) return row == 0 ? 2 : row == 1 ? 3 : row == 2 ? 7 : 8;
+    if (g == 4) return row == 0 ? 4 : row == 2 ? 9 : -1;
+    return -1;
+}
+// Four values (colour and alpha gradients): lane 16 r holds the sum of a_r.
+__device__ inline float wave_reduce4(float a0, float a1, float a2, float a3) {
+    float c = fold16(fold32(a0, a2), fold32(a1, a3));  // rows hold a0 a1 a2 a3
+    c += dpp<DPP_ROW_ROR8>(c);
+    c += dpp<DPP_HALF_MIRROR>(c);
+    c += dpp<DPP_XOR2>(c);
+    c += dpp<DPP_XOR1>(c);
+    return c;
+}
+
+__device__ inline void lds_add(float* p, float v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
 __device__ inline double wave_sum_f64(double v) {
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
@@ -274,11 +370,20 @@ __device__ inline double wave_sum_f64(double v) {
 
 // ---------------------------------------------------------------- main kernel
 
+// Contributing entries a wave records in sweep 1 for sweep 2 (per wave, over
+// all chunks). Beyond it, sweep 2 rebuilds and reclassifies the chunk.
+constexpr int CAP2 = 128;
+
 // LDS layout per block.
 template <int MODE>
 struct Smem {
-    uint32_t list[WAVES][CH];                  // (k_local << 2) | class
-    float acc[MODE == MODE_RENDER ? 1 : WAVES][MODE == MODE_RENDER ? 1 : CH * NP];
+    static constexpr int G = MODE == MODE_RENDER ? 1 : WAVES;
+    static constexpr int C2 = MODE == MODE_RENDER ? 1 : CAP2;
+    uint32_t list[WAVES][CH];  // (k_local << 2) | class
+    uint32_t l2k[G][C2];       // sweep-1 record: triangle index in the scene,
+    uint64_t l2on[G][C2];      //   lanes with w > MIN_WEIGHT,
+    uint64_t l2band[G][C2];    //   and those of them on the exact path
+    float acc[G][MODE == MODE_RENDER ? 1 : CH * NP];
     double loss[WAVES];
 };
 
@@ -333,43 +438,41 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
 }
 
 // Per-pixel weight of one triangle: returns false when the pair is skipped
-// (outside the box, classified far outside, or w <= MIN_WEIGHT). For the band
-// pairs it also returns the geometry the backward needs.
-template <bool FAST, bool NEED_GEO>
-__device__ inline bool pair_weight(const float* __restrict__ r, uint32_t cls, int x, int y, Pix p,
-                                   bool valid, float& w, float& cov, bool& band, Geo& g, float rsig,
-                                   float sig) {
+// (outside the box, classified far outside, or w <= MIN_WEIGHT). `band` tells
+// whether the exact path ran, and then `g` holds its geometry.
+template <bool FAST>
+__device__ inline bool pair_weight(const Rec& r, bool full, int x, int y, Pix p, bool valid, float& w,
+                                   float& cov, bool& band, Geo& g, float rsig, float sig) {
     band = false;
     if (!valid) return false;
-    float alpha = r[R_A];
-    if (cls == CLS_FULL) {
+    const float alpha = r.f(R_A);
+    if (full) {
         cov = 1.0f;
         w = alpha;
-    } else {
-        const int* ri = reinterpret_cast<const int*>(r);
-        if (!(x >= ri[R_BOX] && x < ri[R_BOX + 2] && y >= ri[R_BOX + 1] && y < ri[R_BOX + 3]))
-            return false;
-        bool exact = true;
-        if (ri[R_FLAGS] & F_FAST) {
-            float l0 = fmaf(p.px, r[R_N + 0], fmaf(p.py, r[R_N + 1], -r[R_OFF + 0]));
-            float l1 = fmaf(p.px, r[R_N + 2], fmaf(p.py, r[R_N + 3], -r[R_OFF + 1]));
-            float l2 = fmaf(p.px, r[R_N + 4], fmaf(p.py, r[R_N + 5], -r[R_OFF + 2]));
-            float lm = fmaxf(fmaxf(l0, l1), l2);
-            if (lm > r[R_FAR]) return false;
-            if (lm < r[R_DEEP]) {
-                cov = 1.0f;
-                w = alpha;
-                exact = false;
-            }
-        }
-        if (exact) {
-            g = geometry(r, p, FAST && (ri[R_FLAGS] & F_FAST));
-            float x_ = FAST ? g.sd * rsig : g.sd / sig;
-            cov = sigmoid_f<FAST>(x_);
-            w = alpha * cov;
-            band = true;
-        }
+        return !(w <= MIN_WEIGHT);
     }
+    if (!(x >= r.i(R_BOX) && x < r.i(R_BOX + 2) && y >= r.i(R_BOX + 1) && y < r.i(R_BOX + 3))) return false;
+    if (FAST && (r.i(R_FLAGS) & F_FAST)) {
+        // Conservative classification by the outward edge-line distances.
+        float l0 = fmaf(p.px, r.f(R_N + 0), fmaf(p.py, r.f(R_N + 1), -r.f(R_OFF + 0)));
+        float l1 = fmaf(p.px, r.f(R_N + 2), fmaf(p.py, r.f(R_N + 3), -r.f(R_OFF + 1)));
+        float l2 = fmaf(p.px, r.f(R_N + 4), fmaf(p.py, r.f(R_N + 5), -r.f(R_OFF + 2)));
+        float lm = fmaxf(fmaxf(l0, l1), l2);
+        if (lm > r.f(R_FAR)) return false;
+        if (lm < r.f(R_DEEP)) {
+            cov = 1.0f;
+            w = alpha;
+            return !(w <= MIN_WEIGHT);
+        }
+        g = geometry<true>(r, p);
+        cov = sigmoid_f<true>(g.sd * rsig);
+    } else {
+        asm volatile("");
+        g = geometry<false>(r, p);
+        cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
+    }
+    w = alpha * cov;
+    band = true;
     return !(w <= MIN_WEIGHT);
 }
 
@@ -398,8 +501,76 @@ __device__ inline float trans_suffix(const Trans& total, const Trans& prefix) {
     return ldexpf(ratio, -64 * (total.e - prefix.e));
 }
 
+// Per-pixel state of the backward sweep.
+struct Back {
+    float g0[3];   // dL/dpixel
+    float col[3];  // canvas before the current layer
+    Trans pre;     // transmittance through the current layer
+    Trans tot;     // transmittance of the whole stack
+};
+
+// The backward of one triangle at this lane's pixel (grad.rs:148-181) into the
+// lane's partial gradient `a` (zero where the lane does not contribute).
+__device__ inline void grad_pixel(const Rec& r, bool on, bool band, float w, float cov, const Geo& g, Pix p,
+                                  float rsig, Back& st, float (&a)[NP]) {
+    for (int j = 0; j < NP; j++) a[j] = 0.0f;
+    if (!on) return;
+    float omw = 1.0f - w;
+    trans_mul(st.pre, omw);
+    float tk = trans_suffix(st.tot, st.pre);
+    float d_w = 0.0f;
+    for (int ch = 0; ch < 3; ch++) {
+        float gk = st.g0[ch] * tk;  // d_canvas as the reference holds it at layer k
+        a[6 + ch] = gk * w;
+        d_w = fmaf(gk, r.f(R_C + ch) - st.col[ch], d_w);
+        st.col[ch] = r.f(R_C + ch) * w + st.col[ch] * omw;
+    }
+    if (r.i(R_FLAGS) & F_ACTIVE) a[9] = d_w * cov;
+    float d_cov = d_w * r.f(R_A);
+    // grad.rs:252-268: vertex terms, zero exactly on the boundary.
+    if (band && g.dist >= 1e-9f) {
+        // u = (pt - cp) / dist with cp = a + t (b - a), rounded as
+        // grad.rs:256-259 does: for a pixel within ~1e-7 of an edge the
+        // direction is set by these roundings, and the reference's gradient
+        // inherits them.
+        float inv = __builtin_amdgcn_rcpf(g.dist);
+        float cpx = g.ax + g.t * g.ex, cpy = g.ay + g.t * g.ey;
+        float ux = (p.px - cpx) * inv, uy = (p.py - cpy) * inv;
+        float sgn = g.sd > 0.0f ? 1.0f : -1.0f;
+        float chain = d_cov * cov * (1.0f - cov) * rsig * sgn;
+        float A = -(1.0f - g.t) * chain;  // onto the edge's first vertex
+        float Bc = -g.t * chain;           // onto its second vertex
+        float s0 = g.edge == 0 ? A : (g.edge == 2 ? Bc : 0.0f);
+        float s1 = g.edge == 1 ? A : (g.edge == 0 ? Bc : 0.0f);
+        float s2 = g.edge == 2 ? A : (g.edge == 1 ? Bc : 0.0f);
+        a[0] = s0 * ux;
+        a[1] = s0 * uy;
+        a[2] = s1 * ux;
+        a[3] = s1 * uy;
+        a[4] = s2 * ux;
+        a[5] = s2 * uy;
+    }
+}
+
+// Wave sum of the lanes' partial gradients of one triangle, added to its row
+// of the per-wave accumulator. Within a wave the entries are sequential, so
+// each accumulator receives its adds in list order: the sums are reproducible
+// run to run. `any_band` (wave-uniform) says whether any vertex term is set.
+__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, float* dst, int lane, int p10) {
+    if (any_band) {
+        float e = wave_reduce10(a, lane);
+        if (p10 >= 0) lds_add(dst + p10, e);
+    } else {
+        float e = wave_reduce4(a[6], a[7], a[8], a[9]);
+        if ((lane & 15) == 0) lds_add(dst + 6 + (lane >> 4), e);
+    }
+}
+
+// One wave per 8x8 tile, four tiles (2x2) per block. `records` is also in
+// `a`; passing it as its own const __restrict__ argument tells the compiler
+// that the kernel's stores never alias it.
 template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a, const float* __restrict__ records) {
     __shared__ Smem<MODE> sm;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -417,12 +588,12 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
     p.px = ((float)x + 0.5f) / (float)W;
     p.py = ((float)y + 0.5f) / (float)H;
     // Corners of the tile's pixel-centre rectangle, for the list classification.
-    float cx0 = ((float)tx0 + 0.5f) / (float)W, cy0 = ((float)ty0 + 0.5f) / (float)H;
-    float cx1 = ((float)(tx1 - 1) + 0.5f) / (float)W, cy1 = ((float)(ty1 - 1) + 0.5f) / (float)H;
+    const float cx0 = ((float)tx0 + 0.5f) / (float)W, cy0 = ((float)ty0 + 0.5f) / (float)H;
+    const float cx1 = ((float)(tx1 - 1) + 0.5f) / (float)W, cy1 = ((float)(ty1 - 1) + 0.5f) / (float)H;
 
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
-    const float* __restrict__ rec = a.rec + (size_t)b * T * REC;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
     const size_t pix = ((size_t)b * H + (valid ? y : 0)) * W + (valid ? x : 0);
 
     float col[3];
@@ -432,28 +603,44 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
     Trans tot = {1.0f, 0, 0};
 
     const int n_chunks = (T + CH - 1) / CH;
-    int count = 0;
+    int n2 = 0;                 // contributing entries seen (recorded while n2 < CAP2)
+    int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
 
     // ---- sweep 1: composite in scene order (raster.rs:37-68)
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
-        if (tile_live)
-            count = build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane);
-        else
-            count = 0;
+        int count = tile_live
+                        ? build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane)
+                        : 0;
+        uint32_t nxt = sm.list[wave][0];  // the next entry is read one iteration ahead
         for (int i = 0; i < count; i++) {
-            uint32_t ent = __builtin_amdgcn_readfirstlane(sm.list[wave][i]);
-            int k = k0 + (int)(ent >> 2);
-            const float* r = rec + (size_t)k * REC;
-            float w, cov;
+            const uint32_t ent = __builtin_amdgcn_readfirstlane(nxt);
+            nxt = sm.list[wave][min(i + 1, CH - 1)];
+            const int k = k0 + (int)(ent >> 2);
+            const Rec r = load_rec(rec + (size_t)k * REC);
+            float w = 0.0f, cov;
             bool band;
             Geo g;
-            if (pair_weight<FAST, false>(r, ent & 3u, x, y, p, valid, w, cov, band, g, rsig, sig)) {
+            bool on = pair_weight<FAST>(r, (ent & 3u) == CLS_FULL, x, y, p, valid, w, cov, band, g, rsig, sig);
+            if (on) {
                 float omw = 1.0f - w;
-                for (int ch = 0; ch < 3; ch++) col[ch] = r[R_C + ch] * w + col[ch] * omw;
+                for (int ch = 0; ch < 3; ch++) col[ch] = r.f(R_C + ch) * w + col[ch] * omw;
                 if (MODE != MODE_RENDER) trans_mul(tot, omw);
             }
+            if (MODE != MODE_RENDER) {
+                uint64_t onm = __ballot(on);
+                if (onm != 0) {
+                    uint64_t bm = __ballot(on && band);
+                    if (n2 < CAP2 && lane == 0) {
+                        sm.l2k[wave][n2] = (uint32_t)k;
+                        sm.l2on[wave][n2] = onm;
+                        sm.l2band[wave][n2] = bm;
+                    }
+                    n2++;
+                }
+            }
         }
+        if (n2 > CAP2 && rec_chunks == n_chunks) rec_chunks = c;
     }
 
     if (MODE == MODE_RENDER) {
@@ -466,7 +653,8 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
     }
 
     // ---- dL/dpixel (grad.rs:111-114) and the loss (canvas.rs:45-58)
-    float g0[3] = {0.0f, 0.0f, 0.0f};
+    Back st;
+    st.g0[0] = st.g0[1] = st.g0[2] = 0.0f;
     if (MODE == MODE_LOSS) {
         double l = 0.0;
         if (valid) {
@@ -475,7 +663,7 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
                 float t = a.target[pix * 3 + ch];
                 float d = col[ch] - t;
                 l += (double)d * (double)d;
-                g0[ch] = scale * (col[ch] - t);
+                st.g0[ch] = scale * (col[ch] - t);
             }
         }
         l = wave_sum_f64(l);
@@ -487,96 +675,81 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
         }
     } else {
         if (valid)
-            for (int ch = 0; ch < 3; ch++) g0[ch] = a.grad_in[pix * 3 + ch];
+            for (int ch = 0; ch < 3; ch++) st.g0[ch] = a.grad_in[pix * 3 + ch];
     }
 
     // ---- sweep 2: gradients, again in scene order
     const size_t blk = ((size_t)b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-    col[0] = a.bg[b * 3 + 0];
-    col[1] = a.bg[b * 3 + 1];
-    col[2] = a.bg[b * 3 + 2];
-    Trans pre = {1.0f, 0, 0};
+    st.col[0] = a.bg[b * 3 + 0];
+    st.col[1] = a.bg[b * 3 + 1];
+    st.col[2] = a.bg[b * 3 + 2];
+    st.pre = {1.0f, 0, 0};
+    st.tot = tot;
     float* accw = sm.acc[wave];
+    const int p10 = red10_param(lane);
+    int i2 = 0;
+    const int n2r = min(n2, CAP2);
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
         int nk = k1 - k0;
         for (int j = lane; j < nk * NP; j += 64) accw[j] = 0.0f;
-        if (n_chunks > 1) {
-            if (tile_live)
-                count = build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane);
-            else
-                count = 0;
-        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-        for (int i = 0; i < count; i++) {
-            uint32_t ent = __builtin_amdgcn_readfirstlane(sm.list[wave][i]);
-            int kl = (int)(ent >> 2);
-            const float* r = rec + (size_t)(k0 + kl) * REC;
-            float w = 0.0f, cov = 0.0f;
-            bool band = false;
-            Geo g;
-            bool on = pair_weight<FAST, true>(r, ent & 3u, x, y, p, valid, w, cov, band, g, rsig, sig);
-            float gc[3] = {0.0f, 0.0f, 0.0f}, ga = 0.0f;
-            float gv[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-            if (on) {
-                float omw = 1.0f - w;
-                trans_mul(pre, omw);
-                float tk = trans_suffix(tot, pre);
-                float d_w = 0.0f;
-                for (int ch = 0; ch < 3; ch++) {
-                    float gk = g0[ch] * tk;  // d_canvas as the reference holds it at layer k
-                    gc[ch] = gk * w;
-                    d_w = fmaf(gk, r[R_C + ch] - col[ch], d_w);
-                    col[ch] = r[R_C + ch] * w + col[ch] * omw;
+        if (c < rec_chunks) {
+            // The entries sweep 1 recorded: which lanes contribute and which of
+            // them took the exact path are known, only w is recomputed.
+            uint32_t nk2 = sm.l2k[wave][min(i2, CAP2 - 1)];
+            uint64_t non = sm.l2on[wave][min(i2, CAP2 - 1)], nbm = sm.l2band[wave][min(i2, CAP2 - 1)];
+            for (; i2 < n2r; i2++) {
+                const int k = (int)__builtin_amdgcn_readfirstlane(nk2);
+                if (k >= k1) break;
+                const uint32_t on_lo = __builtin_amdgcn_readfirstlane((uint32_t)non);
+                const uint32_t on_hi = __builtin_amdgcn_readfirstlane((uint32_t)(non >> 32));
+                const uint32_t b_lo = __builtin_amdgcn_readfirstlane((uint32_t)nbm);
+                const uint32_t b_hi = __builtin_amdgcn_readfirstlane((uint32_t)(nbm >> 32));
+                const int i3 = min(i2 + 1, CAP2 - 1);  // the next record entry, read one iteration ahead
+                nk2 = sm.l2k[wave][i3];
+                non = sm.l2on[wave][i3];
+                nbm = sm.l2band[wave][i3];
+                const bool on = ((lane < 32 ? on_lo : on_hi) >> (lane & 31)) & 1u;
+                const bool band = ((lane < 32 ? b_lo : b_hi) >> (lane & 31)) & 1u;
+                const Rec r = load_rec(rec + (size_t)k * REC);
+                float w = 0.0f, cov = 0.0f;
+                Geo g;
+                if (on) {
+                    if (band) {
+                        exact_cov<FAST>(r, p, rsig, sig, g, cov);
+                        w = r.f(R_A) * cov;
+                    } else {
+                        cov = 1.0f;
+                        w = r.f(R_A);
+                    }
                 }
-                const int* ri = reinterpret_cast<const int*>(r);
-                if (ri[R_FLAGS] & F_ACTIVE) ga = d_w * cov;
-                float d_cov = d_w * r[R_A];
-                // grad.rs:252-268: vertex terms, zero exactly on the boundary.
-                if (band && g.dist >= 1e-9f) {
-                    // u = (pt - cp) / dist with cp = a + t (b - a), rounded as
-                    // grad.rs:256-259 does: for a pixel within ~1e-7 of an edge
-                    // the direction is set by these roundings, and the
-                    // reference's gradient inherits them.
-                    float inv = __builtin_amdgcn_rcpf(g.dist);
-                    float cpx = g.ax + g.t * g.ex, cpy = g.ay + g.t * g.ey;
-                    float ux = (p.px - cpx) * inv, uy = (p.py - cpy) * inv;
-                    float sgn = g.sd > 0.0f ? 1.0f : -1.0f;
-                    float chain = d_cov * cov * (1.0f - cov) * rsig * sgn;
-                    float A = -(1.0f - g.t) * chain;  // onto the edge's first vertex
-                    float Bc = -g.t * chain;           // onto its second vertex
-                    float s0 = g.edge == 0 ? A : (g.edge == 2 ? Bc : 0.0f);
-                    float s1 = g.edge == 1 ? A : (g.edge == 0 ? Bc : 0.0f);
-                    float s2 = g.edge == 2 ? A : (g.edge == 1 ? Bc : 0.0f);
-                    gv[0] = s0 * ux;
-                    gv[1] = s0 * uy;
-                    gv[2] = s1 * ux;
-                    gv[3] = s1 * uy;
-                    gv[4] = s2 * ux;
-                    gv[5] = s2 * uy;
-                }
+                float part[NP];
+                grad_pixel(r, on, band, w, cov, g, p, rsig, st, part);
+                reduce_entry(part, (b_lo | b_hi) != 0u, accw + (k - k0) * NP, lane, p10);
             }
-            // Uniform branches: skip the reduction when no lane contributed,
-            // and the six vertex sums when no lane was in the band.
-            if (__ballot(on) == 0) continue;
-            float s[NP];
-            s[6] = wave_sum_to_lane63(gc[0]);
-            s[7] = wave_sum_to_lane63(gc[1]);
-            s[8] = wave_sum_to_lane63(gc[2]);
-            s[9] = wave_sum_to_lane63(ga);
-            bool any_band = __ballot(band) != 0;
-            if (any_band) {
-                for (int j = 0; j < 6; j++) s[j] = wave_sum_to_lane63(gv[j]);
-            }
-            if (lane == 63) {
-                float* dst = accw + kl * NP;
-                if (any_band)
-                    for (int j = 0; j < 6; j++) dst[j] += s[j];
-                for (int j = 6; j < NP; j++) dst[j] += s[j];
+        } else {
+            // Fallback when sweep 1 ran out of record space: rebuild the
+            // chunk's list and classify every pair again.
+            int count = tile_live
+                            ? build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane)
+                            : 0;
+            for (int i = 0; i < count; i++) {
+                const uint32_t ent = __builtin_amdgcn_readfirstlane(sm.list[wave][i]);
+                const int kl = (int)(ent >> 2);
+                const Rec r = load_rec(rec + (size_t)(k0 + kl) * REC);
+                float w = 0.0f, cov = 0.0f;
+                bool band = false;
+                Geo g;
+                bool on = pair_weight<FAST>(r, (ent & 3u) == CLS_FULL, x, y, p, valid, w, cov, band, g, rsig, sig);
+                if (__ballot(on) == 0) continue;
+                float part[NP];
+                grad_pixel(r, on, band, w, cov, g, p, rsig, st, part);
+                reduce_entry(part, __ballot(on && band) != 0, accw + kl * NP, lane, p10);
             }
         }
         __syncthreads();
@@ -599,12 +772,15 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a) {
 }
 
 // Sum the per-block partial rows of each scene in block order. One block per
-// (scene, 64 columns); its four waves split the rows and are combined in order.
-__global__ __launch_bounds__(256) void reduce_partials(const float* __restrict__ partials,
-                                                       const double* __restrict__ partial_loss,
-                                                       int nblk, int T, int npix3, float* __restrict__ grads,
-                                                       float* __restrict__ losses) {
-    __shared__ float part[4][64];
+// (scene, 64 columns); its 16 waves each sum a contiguous range of rows (loads
+// unrolled four deep), and the ranges are combined in row order.
+constexpr int RED_WAVES = 16;
+__global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* __restrict__ partials,
+                                                                  const double* __restrict__ partial_loss,
+                                                                  int nblk, int T, int npix3,
+                                                                  float* __restrict__ grads,
+                                                                  float* __restrict__ losses) {
+    __shared__ float part[RED_WAVES][64];
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = T * NP;
@@ -612,13 +788,20 @@ __global__ __launch_bounds__(256) void reduce_partials(const float* __restrict__
     float acc = 0.0f;
     if (col < cols) {
         const float* base = partials + (size_t)b * nblk * cols + col;
-        int r0 = (nblk * wave) / 4, r1 = (nblk * (wave + 1)) / 4;
-        for (int rr = r0; rr < r1; rr++) acc += base[(size_t)rr * cols];
+        int r0 = (nblk * wave) / RED_WAVES, r1 = (nblk * (wave + 1)) / RED_WAVES;
+        int rr = r0;
+        for (; rr + 4 <= r1; rr += 4) {
+            float v0 = base[(size_t)rr * cols], v1 = base[(size_t)(rr + 1) * cols];
+            float v2 = base[(size_t)(rr + 2) * cols], v3 = base[(size_t)(rr + 3) * cols];
+            acc = (((acc + v0) + v1) + v2) + v3;
+        }
+        for (; rr < r1; rr++) acc += base[(size_t)rr * cols];
     }
     part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && col < cols) {
-        float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+        float v = part[0][lane];
+        for (int q = 1; q < RED_WAVES; q++) v += part[q][lane];
         grads[(size_t)b * cols + col] = v;
     }
     if (losses && blockIdx.x == 0 && threadIdx.x == 0) {
@@ -737,13 +920,15 @@ dim3 raster_grid(int B, int W, int H) {
 
 template <int MODE, bool FAST>
 static hipError_t launch_raster_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((raster_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a);
+    hipLaunchKernelGGL((raster_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
     return hipGetLastError();
 }
 
 hipError_t launch_raster(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
-    if (mode == MODE_RENDER) return fast ? launch_raster_t<MODE_RENDER, true>(a, s) : launch_raster_t<MODE_RENDER, false>(a, s);
-    if (mode == MODE_LOSS) return fast ? launch_raster_t<MODE_LOSS, true>(a, s) : launch_raster_t<MODE_LOSS, false>(a, s);
+    if (mode == MODE_RENDER)
+        return fast ? launch_raster_t<MODE_RENDER, true>(a, s) : launch_raster_t<MODE_RENDER, false>(a, s);
+    if (mode == MODE_LOSS)
+        return fast ? launch_raster_t<MODE_LOSS, true>(a, s) : launch_raster_t<MODE_LOSS, false>(a, s);
     return fast ? launch_raster_t<MODE_GRAD_IN, true>(a, s) : launch_raster_t<MODE_GRAD_IN, false>(a, s);
 }
 
@@ -751,8 +936,8 @@ hipError_t launch_reduce(const float* partials, const double* partial_loss, int 
                          int npix3, float* grads, float* losses, hipStream_t s) {
     int cols = T * NP;
     dim3 grid((cols + 63) / 64 > 0 ? (cols + 63) / 64 : 1, B);
-    hipLaunchKernelGGL(reduce_partials, grid, dim3(256), 0, s, partials, partial_loss, nblk, T, npix3, grads,
-                       losses);
+    hipLaunchKernelGGL(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, T, npix3,
+                       grads, losses);
     return hipGetLastError();
 }
 
