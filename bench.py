@@ -105,7 +105,7 @@ def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev):
         t = ctx.read_timings()
     finally:
         ctx.timing(False)
-    return {k: t[f"{k}_ms"] / max(t[f"{k}_n"], 1) for k in ("setup", "raster", "reduce")}
+    return {k: t[f"{k}_ms"] / max(t[f"{k}_n"], 1) for k in ("setup", "raster", "backward", "reduce")}
 
 
 def traffic_from_profiles():

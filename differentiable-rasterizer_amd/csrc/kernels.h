@@ -11,8 +11,11 @@ constexpr int TILE = 8;   // a wave covers an 8x8 pixel tile, one pixel per lane
 constexpr int WAVES = 4;  // waves per block: 2x2 tiles, a 16x16 pixel region
 constexpr int CH = 128;   // triangles per chunk (LDS accumulators are per chunk)
 
-// Per-triangle record, REC floats, written by setup_records.
-constexpr int REC = 40;
+// Per-triangle record, REC floats, written by setup_records. The hot loops
+// load fields [0, REC_HOT) of one record per list entry; the rest is read
+// only while building a tile's list.
+constexpr int REC = 52;
+constexpr int REC_HOT = 40;
 enum RecField : int {
     R_V = 0,       // 6: vertices x0 y0 x1 y1 x2 y2
     R_C = 6,       // 3: colour
@@ -27,10 +30,27 @@ enum RecField : int {
     R_OFF = 34,    // 3: a . n per edge
     R_FAR = 37,    // max outward distance above which w < MIN_WEIGHT
     R_DEEP = 38,   // max outward distance below which coverage == 1.0f
+    R_SLACK = 39,  // rounding slack of the edge-line distances
+    R_D = 40,      // 6: unit edge directions (fast path only)
+    R_SOFF = 46,   // 3: a . d per edge
+    R_LEN = 49,    // 3: |e|
 };
-enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4 };
+// F_CCW: the cross products of inside points are >= 0 (else <= 0).
+enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4, F_CCW = 8 };
 
 enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2 };
+
+// Contributing entries the forward kernel records per tile for the backward
+// kernel (over all chunks); beyond it the backward kernel rebuilds and
+// reclassifies the remaining chunks.
+constexpr int CAP2 = 128;
+
+// Per-pixel state the forward kernel hands to the backward kernel.
+struct PixState {
+    float g0[3];  // dL/dpixel (MODE_LOSS; MODE_GRAD_IN reads the caller's)
+    float q;      // total transmittance: product of the nonzero (1 - w),
+    int z, e;     // the count of zero factors and of 2^64 rescalings of q
+};
 
 struct RasterArgs {
     int B, T, H, W;
@@ -42,6 +62,14 @@ struct RasterArgs {
     float* out_img;        // B*H*W*3 (MODE_RENDER; optional in MODE_LOSS)
     float* partials;       // B*nblk*T*NP
     double* partial_loss;  // B*nblk
+    PixState* pstate;      // B*H*W
+    uint32_t* tl_k;        // ntiles*CAP2: (k << 8) | (plan << 2) | class
+    uint64_t* tl_on;       // ntiles*CAP2: lanes with w > MIN_WEIGHT
+    uint64_t* tl_band;     // ntiles*CAP2: of those, lanes on the exact path
+    int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded
+    float* grads;          // B*T*NP, accumulated with atomics unless deterministic
+    float* losses;         // B (MODE_LOSS)
+    int deterministic;     // per-block partial rows + reduce_partials instead of atomics
 };
 
 // Device-side state of a running fit (fit.rs:197-211).
@@ -61,8 +89,9 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
                            float* best_params, hipStream_t s);
 
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
-                        float* rec, hipStream_t s);
-hipError_t launch_raster(int mode, bool fast, const RasterArgs& a, hipStream_t s);
+                        float* rec, float* zero_grads, hipStream_t s);
+hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
+hipError_t launch_backward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
                          int npix3, float* grads, float* losses, hipStream_t s);
 hipError_t launch_adam(float* params, const float* grads, float* m, float* v, const float* lr, int n,

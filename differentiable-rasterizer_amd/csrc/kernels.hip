@@ -57,9 +57,13 @@ __device__ inline int upper_bound_px(float hi, float pad, int n) {
 }
 
 __global__ void setup_records(const float* __restrict__ params, int n_tri, int W, int H,
-                              float sigma, int tape_mode, float* __restrict__ rec) {
+                              float sigma, int tape_mode, float* __restrict__ rec,
+                              float* __restrict__ zero_grads) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_tri) return;
+    // The backward kernel adds into the gradients: they start at zero.
+    if (zero_grads)
+        for (int j = 0; j < NP; j++) zero_grads[(size_t)i * NP + j] = 0.0f;
     const float* p = params + (size_t)i * NP;
     float* r = rec + (size_t)i * REC;
 
@@ -131,7 +135,8 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
     ri[R_BOX + 2] = live ? bx1 : 0;
     ri[R_BOX + 3] = live ? by1 : 0;
     bool active = p[9] > 0.0f && p[9] < 1.0f;  // grad.rs:145
-    ri[R_FLAGS] = (live ? F_LIVE : 0) | (active ? F_ACTIVE : 0) | (fast && live ? F_FAST : 0);
+    ri[R_FLAGS] = (live ? F_LIVE : 0) | (active ? F_ACTIVE : 0) | (fast && live ? F_FAST : 0) |
+                  (area2 >= 0.0f ? F_CCW : 0);
     r[R_SPARE] = 0.0f;
     for (int j = 0; j < 6; j++) r[R_E + j] = e[j];
     for (int j = 0; j < 3; j++) r[R_LEN2 + j] = len2[j];
@@ -147,7 +152,19 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
     float xfar = fmaxf(logf(alpha * (1.0f / MIN_WEIGHT)) + 0.05f, 0.0f);
     r[R_FAR] = (xfar == xfar ? xfar : 0.0f) * sig + slack;
     r[R_DEEP] = -(17.0f * sig + slack);
-    for (int j = R_DEEP + 1; j < REC; j++) r[j] = 0.0f;
+    r[R_SLACK] = slack;
+    // Along-edge coordinate s_j = p . d_j - a_j . d_j, with d_j the unit edge
+    // direction: with the edge-line distance it bounds the distance of a whole
+    // tile to each edge segment when the tile's list is built.
+    for (int j = 0; j < 3; j++) {
+        float len = sqrtf(len2[j]);
+        float inv = (fast && len > 0.0f) ? 1.0f / len : 0.0f;
+        float dx = e[2 * j] * inv, dy = e[2 * j + 1] * inv;
+        r[R_D + 2 * j] = dx;
+        r[R_D + 2 * j + 1] = dy;
+        r[R_SOFF + j] = v[2 * j] * dx + v[2 * j + 1] * dy;
+        r[R_LEN + j] = len;
+    }
 }
 
 // ---------------------------------------------------------------- per-pair math
@@ -157,7 +174,7 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
 // entry costs one scalar-memory round trip instead of one per field.
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f8v __attribute__((ext_vector_type(8)));
-static_assert(REC == 40, "load_rec reads 16 + 16 + 8 floats");
+static_assert(REC_HOT == 40 && REC >= REC_HOT, "load_rec reads 16 + 16 + 8 floats");
 struct Rec {
     f16v a, b;
     f8v c;
@@ -283,18 +300,64 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
     return g;
 }
 
-// Exact-path coverage of one pair. The branch on the triangle's F_FAST flag is
-// wave-uniform; the empty volatile asm keeps the compiler from if-converting
-// it, which would evaluate both quotient and square-root variants every time.
+// Entry plans. Built per (tile, triangle) with the tile's list: PLAN_GENERAL,
+// or edge j (0-2) when j is provably the nearest edge for every pixel of the
+// tile and the other two edge lines stay clear of it, so the signs of their
+// cross products are the same at every pixel (inner side when PLAN_INNER).
+enum : uint32_t { PLAN_GENERAL = 3, PLAN_INNER = 4 };
+
+// geometry<true> for a single-edge plan: the reference's distance to edge j
+// and its cross product, with the other edges' results known. The excluded
+// edges are strictly farther (by a margin well above rounding) at every pixel,
+// so the reference's first-minimum selection picks j with the same distance,
+// and the inside test reduces to the sign of c_j.
+__device__ inline Geo geometry1(const Rec& r, Pix p, uint32_t plan) {
+    const int j = (int)(plan & 3u);
+    const float ax = j == 0 ? r.f(R_V + 0) : (j == 1 ? r.f(R_V + 2) : r.f(R_V + 4));
+    const float ay = j == 0 ? r.f(R_V + 1) : (j == 1 ? r.f(R_V + 3) : r.f(R_V + 5));
+    const float ex = j == 0 ? r.f(R_E + 0) : (j == 1 ? r.f(R_E + 2) : r.f(R_E + 4));
+    const float ey = j == 0 ? r.f(R_E + 1) : (j == 1 ? r.f(R_E + 3) : r.f(R_E + 5));
+    const float len2 = j == 0 ? r.f(R_LEN2 + 0) : (j == 1 ? r.f(R_LEN2 + 1) : r.f(R_LEN2 + 2));
+    const float rl = j == 0 ? r.f(R_RLEN2 + 0) : (j == 1 ? r.f(R_RLEN2 + 1) : r.f(R_RLEN2 + 2));
+    const float apx = p.px - ax, apy = p.py - ay;
+    const float c = ex * apy - ey * apx;
+    const float dot = apx * ex + apy * ey;
+    const float q0 = dot * rl;
+    const float res = fmaf(-q0, len2, dot);
+    Geo g;
+    g.t = __builtin_amdgcn_fmed3f(fmaf(res, rl, q0), 0.0f, 1.0f);
+    const float dx = apx - g.t * ex;
+    const float dy = apy - g.t * ey;
+    g.dist = __builtin_amdgcn_sqrtf(dx * dx + dy * dy);
+    const bool ccw = (r.i(R_FLAGS) & F_CCW) != 0;
+    const bool inside = (plan & PLAN_INNER) && (ccw ? c >= 0.0f : c <= 0.0f);
+    g.sd = inside ? g.dist : -g.dist;
+    g.edge = j;
+    g.ax = ax;
+    g.ay = ay;
+    g.ex = ex;
+    g.ey = ey;
+    return g;
+}
+
+// Exact-path coverage of one pair. The branches on the triangle's F_FAST flag
+// and on the plan are wave-uniform; the empty volatile asm keeps the compiler
+// from if-converting them, which would evaluate every variant every time.
 template <bool FAST>
-__device__ inline void exact_cov(const Rec& r, Pix p, float rsig, float sig, Geo& g, float& cov) {
+__device__ inline void exact_cov(const Rec& r, Pix p, uint32_t plan, float rsig, float sig, Geo& g, float& cov) {
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
-        g = geometry<true>(r, p);
+        if ((plan & 3u) != PLAN_GENERAL) {
+            g = geometry1(r, p, plan);
+        } else {
+            asm volatile("");
+            g = geometry<true>(r, p);
+        }
+        cov = sigmoid_f<true>(g.sd * rsig);
     } else {
         asm volatile("");
         g = geometry<false>(r, p);
+        cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
     }
-    cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
 }
 
 // ---------------------------------------------------------------- wave reductions
@@ -359,6 +422,13 @@ __device__ inline float wave_reduce4(float a0, float a1, float a2, float a3) {
     return c;
 }
 
+// Wave-uniform copies of values every lane holds (loaded from one address).
+// The builtin returns int: widen through uint32_t, never by sign extension.
+__device__ inline uint32_t uniform_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ inline uint64_t uniform_u64(uint64_t v) {
+    return ((uint64_t)uniform_u32((uint32_t)(v >> 32)) << 32) | (uint64_t)uniform_u32((uint32_t)v);
+}
+
 __device__ inline void lds_add(float* p, float v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
@@ -368,37 +438,27 @@ __device__ inline double wave_sum_f64(double v) {
     return v;
 }
 
-// ---------------------------------------------------------------- main kernel
-
-// Contributing entries a wave records in sweep 1 for sweep 2 (per wave, over
-// all chunks). Beyond it, sweep 2 rebuilds and reclassifies the chunk.
-constexpr int CAP2 = 128;
-
-// LDS layout per block.
-template <int MODE>
-struct Smem {
-    static constexpr int G = MODE == MODE_RENDER ? 1 : WAVES;
-    static constexpr int C2 = MODE == MODE_RENDER ? 1 : CAP2;
-    uint32_t list[WAVES][CH];  // (k_local << 2) | class
-    uint32_t l2k[G][C2];       // sweep-1 record: triangle index in the scene,
-    uint64_t l2on[G][C2];      //   lanes with w > MIN_WEIGHT,
-    uint64_t l2band[G][C2];    //   and those of them on the exact path
-    float acc[G][MODE == MODE_RENDER ? 1 : CH * NP];
-    double loss[WAVES];
-};
+// ---------------------------------------------------------------- forward and backward kernels
 
 enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 
 // Builds this wave's ordered list of triangles in [k0, k1) that can touch its
-// tile, with a class per entry: FULL when every tile pixel is inside the
-// triangle's box and deep inside the triangle, else PARTIAL.
+// tile. Entry: (k_local << 8) | (plan << 2) | class, with class FULL when every
+// tile pixel is inside the triangle's box and deep inside the triangle, else
+// PARTIAL, and the plan of the exact path (PLAN_* or a single edge).
+//
+// Plans use bounds over the tile's pixel-centre rectangle: with l the outward
+// edge-line distance and s the along-edge coordinate (both affine, so extreme
+// at the corners), the distance to segment j is sqrt(l^2 + ex^2) with
+// ex = max(0, -s, s - |e|). An edge whose lower bound exceeds the smallest
+// upper bound by more than the margin is never nearest.
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
                                  uint32_t* list, int lane) {
     int count = 0;
     for (int base = k0; base < k1; base += 64) {
         int k = base + lane;
-        uint32_t cls = 0;
+        uint32_t cls = 0, plan = PLAN_GENERAL;
         if (k < k1) {
             const float* r = rec + (size_t)k * REC;
             const int* ri = reinterpret_cast<const int*>(r);
@@ -408,6 +468,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                 cls = CLS_PARTIAL;
                 if (flags & F_FAST) {
                     float far = r[R_FAR], deep = r[R_DEEP];
+                    float lmin[3], lmax[3];
                     bool culled = false, all_deep = true;
                     for (int j = 0; j < 3; j++) {
                         float nx = r[R_N + 2 * j], ny = r[R_N + 2 * j + 1], o = r[R_OFF + j];
@@ -415,14 +476,56 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                         float l10 = fmaf(cx1, nx, fmaf(cy0, ny, -o));
                         float l01 = fmaf(cx0, nx, fmaf(cy1, ny, -o));
                         float l11 = fmaf(cx1, nx, fmaf(cy1, ny, -o));
-                        float lmin = fminf(fminf(l00, l10), fminf(l01, l11));
-                        float lmax = fmaxf(fmaxf(l00, l10), fmaxf(l01, l11));
-                        culled = culled || (lmin > far);
-                        all_deep = all_deep && (lmax < deep);
+                        lmin[j] = fminf(fminf(l00, l10), fminf(l01, l11));
+                        lmax[j] = fmaxf(fmaxf(l00, l10), fmaxf(l01, l11));
+                        culled = culled || (lmin[j] > far);
+                        all_deep = all_deep && (lmax[j] < deep);
                     }
                     bool in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
-                    if (culled) cls = 0;
-                    else if (all_deep && in_box) cls = CLS_FULL;
+                    if (culled) {
+                        cls = 0;
+                    } else if (all_deep && in_box) {
+                        cls = CLS_FULL;
+                    } else {
+                        const float slack = r[R_SLACK];
+                        float lb[3], ubmin = INFINITY;
+                        for (int j = 0; j < 3; j++) {
+                            float dx = r[R_D + 2 * j], dy = r[R_D + 2 * j + 1], so = r[R_SOFF + j];
+                            float len = r[R_LEN + j];
+                            float s00 = fmaf(cx0, dx, fmaf(cy0, dy, -so));
+                            float s10 = fmaf(cx1, dx, fmaf(cy0, dy, -so));
+                            float s01 = fmaf(cx0, dx, fmaf(cy1, dy, -so));
+                            float s11 = fmaf(cx1, dx, fmaf(cy1, dy, -so));
+                            float smin = fminf(fminf(s00, s10), fminf(s01, s11));
+                            float smax = fmaxf(fmaxf(s00, s10), fmaxf(s01, s11));
+                            float exmin = fmaxf(fmaxf(-smax, smin - len), 0.0f);
+                            float exmax = fmaxf(fmaxf(-smin, smax - len), 0.0f);
+                            float la = (lmin[j] <= 0.0f && lmax[j] >= 0.0f)
+                                           ? 0.0f
+                                           : fminf(fabsf(lmin[j]), fabsf(lmax[j]));
+                            float lz = fmaxf(fabsf(lmin[j]), fabsf(lmax[j]));
+                            lb[j] = sqrtf(la * la + exmin * exmin);
+                            ubmin = fminf(ubmin, sqrtf(lz * lz + exmax * exmax));
+                        }
+                        // The reference's rounded distances are within ~1e-7 (1 + max |v|)
+                        // of these bounds' exact values; 0.1 slack is ten times that.
+                        const float lim = ubmin + 0.1f * slack;
+                        int ncand = 0, jc = 0;
+                        for (int j = 0; j < 3; j++)
+                            if (!(lb[j] > lim)) {
+                                ncand++;
+                                jc = j;
+                            }
+                        if (ncand == 1) {
+                            bool clear = true, inner = true;
+                            for (int j = 0; j < 3; j++) {
+                                if (j == jc) continue;
+                                clear = clear && (lmin[j] > slack || lmax[j] < -slack);
+                                inner = inner && (lmax[j] < -slack);
+                            }
+                            if (clear) plan = (uint32_t)jc | (inner ? PLAN_INNER : 0u);
+                        }
+                    }
                 }
             }
         }
@@ -430,7 +533,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
         if (cls != 0) {
             int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = ((uint32_t)(k - k0) << 2) | cls;
+            list[pos] = ((uint32_t)(k - k0) << 8) | (plan << 2) | cls;
         }
         count += (int)__popcll(mask);
     }
@@ -441,8 +544,9 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
 // (outside the box, classified far outside, or w <= MIN_WEIGHT). `band` tells
 // whether the exact path ran, and then `g` holds its geometry.
 template <bool FAST>
-__device__ inline bool pair_weight(const Rec& r, bool full, int x, int y, Pix p, bool valid, float& w,
+__device__ inline bool pair_weight(const Rec& r, uint32_t ent, int x, int y, Pix p, bool valid, float& w,
                                    float& cov, bool& band, Geo& g, float rsig, float sig) {
+    const bool full = (ent & 3u) == CLS_FULL;
     band = false;
     if (!valid) return false;
     const float alpha = r.f(R_A);
@@ -464,13 +568,8 @@ __device__ inline bool pair_weight(const Rec& r, bool full, int x, int y, Pix p,
             w = alpha;
             return !(w <= MIN_WEIGHT);
         }
-        g = geometry<true>(r, p);
-        cov = sigmoid_f<true>(g.sd * rsig);
-    } else {
-        asm volatile("");
-        g = geometry<false>(r, p);
-        cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
     }
+    exact_cov<FAST>(r, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
     band = true;
     return !(w <= MIN_WEIGHT);
@@ -499,6 +598,148 @@ __device__ inline float trans_suffix(const Trans& total, const Trans& prefix) {
     if (total.z != prefix.z) return 0.0f;
     float ratio = total.q * __builtin_amdgcn_rcpf(prefix.q);
     return ldexpf(ratio, -64 * (total.e - prefix.e));
+}
+
+// Tile geometry shared by both kernels: one wave per 8x8 tile, four tiles
+// (2x2) per block, one pixel per lane.
+struct TileGeo {
+    int lane, wave, b, x, y, tx0, ty0, tx1, ty1;
+    bool valid, live;
+    Pix p;
+    float cx0, cy0, cx1, cy1;
+    size_t pix, tile;
+};
+
+__device__ inline TileGeo tile_geo(int W, int H) {
+    TileGeo t;
+    t.lane = threadIdx.x & 63;
+    t.wave = threadIdx.x >> 6;
+    t.b = blockIdx.z;
+    t.tx0 = (blockIdx.x * 2 + (t.wave & 1)) * TILE;
+    t.ty0 = (blockIdx.y * 2 + (t.wave >> 1)) * TILE;
+    t.x = t.tx0 + (t.lane & 7);
+    t.y = t.ty0 + (t.lane >> 3);
+    t.valid = t.x < W && t.y < H;
+    t.tx1 = min(t.tx0 + TILE, W);
+    t.ty1 = min(t.ty0 + TILE, H);
+    t.live = t.tx0 < W && t.ty0 < H;
+    // raster.rs:138-140 pixel centre, correctly rounded division.
+    t.p.px = ((float)t.x + 0.5f) / (float)W;
+    t.p.py = ((float)t.y + 0.5f) / (float)H;
+    // Corners of the tile's pixel-centre rectangle, for the list classification.
+    t.cx0 = ((float)t.tx0 + 0.5f) / (float)W;
+    t.cy0 = ((float)t.ty0 + 0.5f) / (float)H;
+    t.cx1 = ((float)(t.tx1 - 1) + 0.5f) / (float)W;
+    t.cy1 = ((float)(t.ty1 - 1) + 0.5f) / (float)H;
+    t.pix = ((size_t)t.b * H + (t.valid ? t.y : 0)) * W + (t.valid ? t.x : 0);
+    t.tile = (((size_t)t.b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * WAVES + t.wave;
+    return t;
+}
+
+// Forward: composite in scene order (raster.rs:37-68). In the gradient modes it
+// also keeps each pixel's total transmittance and records, per tile, the
+// entries that contribute at any of its pixels with their lane masks (on,
+// and exact-path), so the backward kernel neither rebuilds nor reclassifies.
+// MODE_LOSS adds the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114).
+template <int MODE, bool FAST>
+__global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
+    __shared__ uint32_t list[WAVES][CH];
+    __shared__ double loss[WAVES];
+    const int W = a.W, H = a.H, T = a.T;
+    const TileGeo tg = tile_geo(W, H);
+    const int lane = tg.lane, wave = tg.wave, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = 1.0f / sig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    float col[3];
+    col[0] = a.bg[b * 3 + 0];
+    col[1] = a.bg[b * 3 + 1];
+    col[2] = a.bg[b * 3 + 2];
+    Trans tot = {1.0f, 0, 0};
+
+    const int n_chunks = (T + CH - 1) / CH;
+    int n2 = 0;                 // contributing entries seen (recorded while n2 < CAP2)
+    int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
+    uint32_t* tk = a.tl_k + tg.tile * CAP2;
+    uint64_t* ton = a.tl_on + tg.tile * CAP2;
+    uint64_t* tband = a.tl_band + tg.tile * CAP2;
+
+    for (int c = 0; c < n_chunks; c++) {
+        int k0 = c * CH, k1 = min(T, k0 + CH);
+        int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0, tg.cx1,
+                                         tg.cy1, list[wave], lane)
+                            : 0;
+        uint32_t nxt = list[wave][0];  // the next entry is read one iteration ahead
+        for (int i = 0; i < count; i++) {
+            const uint32_t ent = uniform_u32(nxt);
+            nxt = list[wave][min(i + 1, CH - 1)];
+            const int k = k0 + (int)(ent >> 8);
+            const Rec r = load_rec(rec + (size_t)k * REC);
+            float w = 0.0f, cov;
+            bool band;
+            Geo g;
+            bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+            if (on) {
+                float omw = 1.0f - w;
+                for (int ch = 0; ch < 3; ch++) col[ch] = r.f(R_C + ch) * w + col[ch] * omw;
+                if (MODE != MODE_RENDER) trans_mul(tot, omw);
+            }
+            if (MODE != MODE_RENDER) {
+                uint64_t onm = __ballot(on);
+                if (onm != 0) {
+                    uint64_t bm = __ballot(on && band);
+                    if (n2 < CAP2 && lane == 0) {
+                        tk[n2] = ((uint32_t)k << 8) | (ent & 0xFFu);
+                        ton[n2] = onm;
+                        tband[n2] = bm;
+                    }
+                    n2++;
+                }
+            }
+        }
+        if (n2 > CAP2 && rec_chunks == n_chunks) rec_chunks = c;
+    }
+
+    if (MODE == MODE_RENDER || (MODE == MODE_LOSS && a.out_img)) {
+        if (tg.valid) {
+            a.out_img[tg.pix * 3 + 0] = col[0];
+            a.out_img[tg.pix * 3 + 1] = col[1];
+            a.out_img[tg.pix * 3 + 2] = col[2];
+        }
+    }
+    if (MODE == MODE_RENDER) return;
+
+    if (lane == 0) {
+        a.tl_n[2 * tg.tile] = min(n2, CAP2);
+        a.tl_n[2 * tg.tile + 1] = rec_chunks;
+    }
+    PixState ps;
+    ps.g0[0] = ps.g0[1] = ps.g0[2] = 0.0f;
+    ps.q = tot.q;
+    ps.z = tot.z;
+    ps.e = tot.e;
+    if (MODE == MODE_LOSS) {
+        double l = 0.0;
+        if (tg.valid) {
+            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            for (int ch = 0; ch < 3; ch++) {
+                float t = a.target[tg.pix * 3 + ch];
+                float d = col[ch] - t;
+                l += (double)d * (double)d;
+                ps.g0[ch] = scale * (col[ch] - t);
+            }
+        }
+        l = wave_sum_f64(l);
+        if (lane == 0) loss[wave] = l;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double lb = loss[0];
+            for (int q = 1; q < WAVES; q++) lb += loss[q];
+            a.partial_loss[tg.tile / WAVES] = lb;
+        }
+    }
+    if (tg.valid) a.pstate[tg.pix] = ps;
 }
 
 // Per-pixel state of the backward sweep.
@@ -566,129 +807,46 @@ __device__ inline void reduce_entry(const float (&a)[NP], bool any_band, float* 
     }
 }
 
-// One wave per 8x8 tile, four tiles (2x2) per block. `records` is also in
-// `a`; passing it as its own const __restrict__ argument tells the compiler
-// that the kernel's stores never alias it.
+// Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
+// forward kernel recorded, again in scene order. The gradient reaching layer
+// k, d_canvas * prod_{j>k} (1 - w_j) (grad.rs:162-169), is formed as a ratio
+// of transmittance products instead of being peeled off a tape. Per-triangle
+// gradients are wave-reduced, accumulated per wave in LDS and written as one
+// partial row per block and chunk.
 template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a, const float* __restrict__ records) {
-    __shared__ Smem<MODE> sm;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int b = blockIdx.z;
+__global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, const float* __restrict__ records) {
+    __shared__ uint32_t list[WAVES][CH];
+    __shared__ float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
-    const int tx0 = (blockIdx.x * 2 + (wave & 1)) * TILE;
-    const int ty0 = (blockIdx.y * 2 + (wave >> 1)) * TILE;
-    const int x = tx0 + (lane & 7), y = ty0 + (lane >> 3);
-    const bool valid = x < W && y < H;
-    const int tx1 = min(tx0 + TILE, W), ty1 = min(ty0 + TILE, H);
-    const bool tile_live = tx0 < W && ty0 < H;
-
-    // raster.rs:138-140 pixel centre, correctly rounded division.
-    Pix p;
-    p.px = ((float)x + 0.5f) / (float)W;
-    p.py = ((float)y + 0.5f) / (float)H;
-    // Corners of the tile's pixel-centre rectangle, for the list classification.
-    const float cx0 = ((float)tx0 + 0.5f) / (float)W, cy0 = ((float)ty0 + 0.5f) / (float)H;
-    const float cx1 = ((float)(tx1 - 1) + 0.5f) / (float)W, cy1 = ((float)(ty1 - 1) + 0.5f) / (float)H;
-
+    const TileGeo tg = tile_geo(W, H);
+    const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
-    const size_t pix = ((size_t)b * H + (valid ? y : 0)) * W + (valid ? x : 0);
 
-    float col[3];
-    col[0] = a.bg[b * 3 + 0];
-    col[1] = a.bg[b * 3 + 1];
-    col[2] = a.bg[b * 3 + 2];
-    Trans tot = {1.0f, 0, 0};
-
-    const int n_chunks = (T + CH - 1) / CH;
-    int n2 = 0;                 // contributing entries seen (recorded while n2 < CAP2)
-    int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
-
-    // ---- sweep 1: composite in scene order (raster.rs:37-68)
-    for (int c = 0; c < n_chunks; c++) {
-        int k0 = c * CH, k1 = min(T, k0 + CH);
-        int count = tile_live
-                        ? build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane)
-                        : 0;
-        uint32_t nxt = sm.list[wave][0];  // the next entry is read one iteration ahead
-        for (int i = 0; i < count; i++) {
-            const uint32_t ent = __builtin_amdgcn_readfirstlane(nxt);
-            nxt = sm.list[wave][min(i + 1, CH - 1)];
-            const int k = k0 + (int)(ent >> 2);
-            const Rec r = load_rec(rec + (size_t)k * REC);
-            float w = 0.0f, cov;
-            bool band;
-            Geo g;
-            bool on = pair_weight<FAST>(r, (ent & 3u) == CLS_FULL, x, y, p, valid, w, cov, band, g, rsig, sig);
-            if (on) {
-                float omw = 1.0f - w;
-                for (int ch = 0; ch < 3; ch++) col[ch] = r.f(R_C + ch) * w + col[ch] * omw;
-                if (MODE != MODE_RENDER) trans_mul(tot, omw);
-            }
-            if (MODE != MODE_RENDER) {
-                uint64_t onm = __ballot(on);
-                if (onm != 0) {
-                    uint64_t bm = __ballot(on && band);
-                    if (n2 < CAP2 && lane == 0) {
-                        sm.l2k[wave][n2] = (uint32_t)k;
-                        sm.l2on[wave][n2] = onm;
-                        sm.l2band[wave][n2] = bm;
-                    }
-                    n2++;
-                }
-            }
-        }
-        if (n2 > CAP2 && rec_chunks == n_chunks) rec_chunks = c;
-    }
-
-    if (MODE == MODE_RENDER) {
-        if (valid) {
-            a.out_img[pix * 3 + 0] = col[0];
-            a.out_img[pix * 3 + 1] = col[1];
-            a.out_img[pix * 3 + 2] = col[2];
-        }
-        return;
-    }
-
-    // ---- dL/dpixel (grad.rs:111-114) and the loss (canvas.rs:45-58)
     Back st;
-    st.g0[0] = st.g0[1] = st.g0[2] = 0.0f;
-    if (MODE == MODE_LOSS) {
-        double l = 0.0;
-        if (valid) {
-            float scale = 2.0f / (float)(3 * (size_t)W * H);
-            for (int ch = 0; ch < 3; ch++) {
-                float t = a.target[pix * 3 + ch];
-                float d = col[ch] - t;
-                l += (double)d * (double)d;
-                st.g0[ch] = scale * (col[ch] - t);
-            }
+    {
+        PixState ps = a.pstate[tg.pix];
+        st.tot = {ps.q, ps.z, ps.e};
+        for (int ch = 0; ch < 3; ch++) {
+            st.g0[ch] = !tg.valid ? 0.0f : (MODE == MODE_LOSS ? ps.g0[ch] : a.grad_in[tg.pix * 3 + ch]);
         }
-        l = wave_sum_f64(l);
-        if (lane == 0) sm.loss[wave] = l;
-        if (a.out_img && valid) {
-            a.out_img[pix * 3 + 0] = col[0];
-            a.out_img[pix * 3 + 1] = col[1];
-            a.out_img[pix * 3 + 2] = col[2];
-        }
-    } else {
-        if (valid)
-            for (int ch = 0; ch < 3; ch++) st.g0[ch] = a.grad_in[pix * 3 + ch];
     }
-
-    // ---- sweep 2: gradients, again in scene order
-    const size_t blk = ((size_t)b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
     st.col[0] = a.bg[b * 3 + 0];
     st.col[1] = a.bg[b * 3 + 1];
     st.col[2] = a.bg[b * 3 + 2];
     st.pre = {1.0f, 0, 0};
-    st.tot = tot;
-    float* accw = sm.acc[wave];
+
+    const int n_chunks = (T + CH - 1) / CH;
+    const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
+    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
+    const uint32_t* tk = a.tl_k + tg.tile * CAP2;
+    const uint64_t* ton = a.tl_on + tg.tile * CAP2;
+    const uint64_t* tband = a.tl_band + tg.tile * CAP2;
+    const size_t blk = tg.tile / WAVES;
+    float* accw = acc[wave];
     const int p10 = red10_param(lane);
     int i2 = 0;
-    const int n2r = min(n2, CAP2);
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -699,29 +857,28 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a, const 
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
         if (c < rec_chunks) {
-            // The entries sweep 1 recorded: which lanes contribute and which of
-            // them took the exact path are known, only w is recomputed.
-            uint32_t nk2 = sm.l2k[wave][min(i2, CAP2 - 1)];
-            uint64_t non = sm.l2on[wave][min(i2, CAP2 - 1)], nbm = sm.l2band[wave][min(i2, CAP2 - 1)];
+            // The entries the forward kernel recorded: which lanes contribute
+            // and which of them took the exact path are known; only w is
+            // recomputed. The next entry is read one iteration ahead.
+            uint32_t nk2 = tk[min(i2, CAP2 - 1)];
+            uint64_t non = ton[min(i2, CAP2 - 1)], nbm = tband[min(i2, CAP2 - 1)];
             for (; i2 < n2r; i2++) {
-                const int k = (int)__builtin_amdgcn_readfirstlane(nk2);
+                const uint32_t e2 = uniform_u32(nk2);
+                const int k = (int)(e2 >> 8);
                 if (k >= k1) break;
-                const uint32_t on_lo = __builtin_amdgcn_readfirstlane((uint32_t)non);
-                const uint32_t on_hi = __builtin_amdgcn_readfirstlane((uint32_t)(non >> 32));
-                const uint32_t b_lo = __builtin_amdgcn_readfirstlane((uint32_t)nbm);
-                const uint32_t b_hi = __builtin_amdgcn_readfirstlane((uint32_t)(nbm >> 32));
-                const int i3 = min(i2 + 1, CAP2 - 1);  // the next record entry, read one iteration ahead
-                nk2 = sm.l2k[wave][i3];
-                non = sm.l2on[wave][i3];
-                nbm = sm.l2band[wave][i3];
-                const bool on = ((lane < 32 ? on_lo : on_hi) >> (lane & 31)) & 1u;
-                const bool band = ((lane < 32 ? b_lo : b_hi) >> (lane & 31)) & 1u;
+                const uint64_t onm = uniform_u64(non), bm = uniform_u64(nbm);
+                const int i3 = min(i2 + 1, CAP2 - 1);
+                nk2 = tk[i3];
+                non = ton[i3];
+                nbm = tband[i3];
+                const bool on = (onm >> lane) & 1u;
+                const bool band = (bm >> lane) & 1u;
                 const Rec r = load_rec(rec + (size_t)k * REC);
                 float w = 0.0f, cov = 0.0f;
                 Geo g;
                 if (on) {
                     if (band) {
-                        exact_cov<FAST>(r, p, rsig, sig, g, cov);
+                        exact_cov<FAST>(r, tg.p, (e2 >> 2) & 7u, rsig, sig, g, cov);
                         w = r.f(R_A) * cov;
                     } else {
                         cov = 1.0f;
@@ -729,45 +886,60 @@ __global__ __launch_bounds__(WAVES * 64) void raster_kernel(RasterArgs a, const 
                     }
                 }
                 float part[NP];
-                grad_pixel(r, on, band, w, cov, g, p, rsig, st, part);
-                reduce_entry(part, (b_lo | b_hi) != 0u, accw + (k - k0) * NP, lane, p10);
+                grad_pixel(r, on, band, w, cov, g, tg.p, rsig, st, part);
+                reduce_entry(part, bm != 0, accw + (k - k0) * NP, lane, p10);
             }
         } else {
-            // Fallback when sweep 1 ran out of record space: rebuild the
-            // chunk's list and classify every pair again.
-            int count = tile_live
-                            ? build_list(rec, k0, k1, tx0, ty0, tx1, ty1, cx0, cy0, cx1, cy1, sm.list[wave], lane)
-                            : 0;
+            // Fallback when the forward kernel ran out of record space: rebuild
+            // the chunk's list and classify every pair again.
+            int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
+                                             tg.cx1, tg.cy1, list[wave], lane)
+                                : 0;
             for (int i = 0; i < count; i++) {
-                const uint32_t ent = __builtin_amdgcn_readfirstlane(sm.list[wave][i]);
-                const int kl = (int)(ent >> 2);
+                const uint32_t ent = uniform_u32(list[wave][i]);
+                const int kl = (int)(ent >> 8);
                 const Rec r = load_rec(rec + (size_t)(k0 + kl) * REC);
                 float w = 0.0f, cov = 0.0f;
                 bool band = false;
                 Geo g;
-                bool on = pair_weight<FAST>(r, (ent & 3u) == CLS_FULL, x, y, p, valid, w, cov, band, g, rsig, sig);
+                bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
                 if (__ballot(on) == 0) continue;
                 float part[NP];
-                grad_pixel(r, on, band, w, cov, g, p, rsig, st, part);
+                grad_pixel(r, on, band, w, cov, g, tg.p, rsig, st, part);
                 reduce_entry(part, __ballot(on && band) != 0, accw + kl * NP, lane, p10);
             }
         }
         __syncthreads();
-        // One partial row per block: the four waves' accumulators summed in
-        // wave order, so the result does not depend on scheduling.
-        float* prow = a.partials + (blk * T + k0) * NP;
-        for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
-            float v = sm.acc[0][j];
-            for (int q = 1; q < WAVES; q++) v += sm.acc[q][j];
-            prow[j] = v;
+        // The block's sums: the four waves' accumulators added in wave order.
+        // Deterministic mode writes them as the block's partial row for
+        // reduce_partials; otherwise each nonzero sum is one native float
+        // atomic add into the output (one per triangle parameter per block).
+        if (a.deterministic) {
+            float* prow = a.partials + (blk * T + k0) * NP;
+            for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
+                float v = acc[0][j];
+                for (int q = 1; q < WAVES; q++) v += acc[q][j];
+                prow[j] = v;
+            }
+        } else {
+            float* grow = a.grads + ((size_t)b * T + k0) * NP;
+            for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
+                float v = acc[0][j];
+                for (int q = 1; q < WAVES; q++) v += acc[q][j];
+                if (v != 0.0f) unsafeAtomicAdd(grow + j, v);
+            }
         }
         __syncthreads();
     }
-    __syncthreads();  // also orders sm.loss when there are no chunks (T == 0)
-    if (MODE == MODE_LOSS && threadIdx.x == 0) {
-        double l = sm.loss[0];
-        for (int q = 1; q < WAVES; q++) l += sm.loss[q];
-        a.partial_loss[blk] = l;
+    // The per-item loss (canvas.rs:45-58) from the forward kernel's per-block
+    // sums, by the scene's first block, in a fixed order.
+    if (MODE == MODE_LOSS && !a.deterministic && blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+        const int nblk = gridDim.x * gridDim.y;
+        const double* pl = a.partial_loss + (size_t)b * nblk;
+        double l = 0.0;
+        for (int r = lane; r < nblk; r += 64) l += pl[r];
+        l = wave_sum_f64(l);
+        if (lane == 0) a.losses[b] = (float)(l / (3.0 * (double)W * (double)H));
     }
 }
 
@@ -804,10 +976,11 @@ __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* _
         for (int q = 1; q < RED_WAVES; q++) v += part[q][lane];
         grads[(size_t)b * cols + col] = v;
     }
-    if (losses && blockIdx.x == 0 && threadIdx.x == 0) {
+    if (losses && blockIdx.x == 0 && wave == 0) {
         double s = 0.0;
-        for (int rr = 0; rr < nblk; rr++) s += partial_loss[(size_t)b * nblk + rr];
-        losses[b] = (float)(s / (double)npix3);
+        for (int rr = lane; rr < nblk; rr += 64) s += partial_loss[(size_t)b * nblk + rr];
+        s = wave_sum_f64(s);
+        if (lane == 0) losses[b] = (float)(s / (double)npix3);
     }
 }
 
@@ -906,11 +1079,11 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
 }
 
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
-                        float* rec, hipStream_t s) {
+                        float* rec, float* zero_grads, hipStream_t s) {
     int n = B * T;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(setup_records, dim3((n + 255) / 256), dim3(256), 0, s, params, n, W, H, sigma,
-                       tape_mode, rec);
+    hipLaunchKernelGGL(setup_records, dim3((n + 63) / 64), dim3(64), 0, s, params, n, W, H, sigma,
+                       tape_mode, rec, zero_grads);
     return hipGetLastError();
 }
 
@@ -919,17 +1092,29 @@ dim3 raster_grid(int B, int W, int H) {
 }
 
 template <int MODE, bool FAST>
-static hipError_t launch_raster_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((raster_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
+static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((forward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
     return hipGetLastError();
 }
 
-hipError_t launch_raster(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
+template <int MODE, bool FAST>
+static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((backward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
+    return hipGetLastError();
+}
+
+hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
     if (mode == MODE_RENDER)
-        return fast ? launch_raster_t<MODE_RENDER, true>(a, s) : launch_raster_t<MODE_RENDER, false>(a, s);
+        return fast ? launch_forward_t<MODE_RENDER, true>(a, s) : launch_forward_t<MODE_RENDER, false>(a, s);
     if (mode == MODE_LOSS)
-        return fast ? launch_raster_t<MODE_LOSS, true>(a, s) : launch_raster_t<MODE_LOSS, false>(a, s);
-    return fast ? launch_raster_t<MODE_GRAD_IN, true>(a, s) : launch_raster_t<MODE_GRAD_IN, false>(a, s);
+        return fast ? launch_forward_t<MODE_LOSS, true>(a, s) : launch_forward_t<MODE_LOSS, false>(a, s);
+    return fast ? launch_forward_t<MODE_GRAD_IN, true>(a, s) : launch_forward_t<MODE_GRAD_IN, false>(a, s);
+}
+
+hipError_t launch_backward(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
+    if (mode == MODE_LOSS)
+        return fast ? launch_backward_t<MODE_LOSS, true>(a, s) : launch_backward_t<MODE_LOSS, false>(a, s);
+    return fast ? launch_backward_t<MODE_GRAD_IN, true>(a, s) : launch_backward_t<MODE_GRAD_IN, false>(a, s);
 }
 
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,

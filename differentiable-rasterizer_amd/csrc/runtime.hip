@@ -53,6 +53,11 @@ enum Kind : uint64_t {
     K_OUT_LOSSES,
     K_FIT_F32,
     K_FIT_STATE,
+    K_PIXSTATE,
+    K_TILE_K,
+    K_TILE_ON,
+    K_TILE_BAND,
+    K_TILE_N,
 };
 
 // Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
@@ -70,7 +75,7 @@ struct PoolBuf {
 }  // namespace
 
 namespace {
-enum TimedKernel : int { TK_SETUP = 0, TK_RASTER, TK_REDUCE, TK_ADAM, TK_COUNT };
+enum TimedKernel : int { TK_SETUP = 0, TK_RASTER, TK_REDUCE, TK_ADAM, TK_BACKWARD, TK_COUNT };
 struct TimedLaunch {
     int kernel;
     hipEvent_t start, stop;
@@ -336,24 +341,33 @@ class KernelTimer {
     bool on_ = false;
 };
 
-// The shared raster sequence: records, one raster pass, and (for the
-// gradient modes) the partial-row reduction.
+// The shared raster sequence: records, the forward pass, and (for the
+// gradient modes) the backward pass and the partial-row reduction.
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
                int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
                hipStream_t s) {
     bool fast = !(flags & DRH_EXACT_MATH);
+    bool det = (flags & DRH_DETERMINISTIC) != 0;
     dim3 grid = drh::raster_grid(B, W, H);
     int nblk = (int)(grid.x * grid.y);
-    Lease rec, partials, ploss;
+    size_t ntiles = (size_t)B * nblk * drh::WAVES;
+    Lease rec, partials, ploss, pstate, tk, ton, tband, tn;
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
     if (mode != drh::MODE_RENDER) {
-        if ((rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s))) return rc;
+        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
+            return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
+        if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
+        if ((rc = tk.acquire(ctx, K_TILE_K, ntiles * drh::CAP2 * sizeof(uint32_t), s))) return rc;
+        if ((rc = ton.acquire(ctx, K_TILE_ON, ntiles * drh::CAP2 * sizeof(uint64_t), s))) return rc;
+        if ((rc = tband.acquire(ctx, K_TILE_BAND, ntiles * drh::CAP2 * sizeof(uint64_t), s))) return rc;
+        if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
     }
     {
         KernelTimer kt(ctx, TK_SETUP, s);
-        HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(), s),
+        HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(),
+                                  mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s),
                 "setup_records launch");
     }
     drh::RasterArgs a{};
@@ -369,11 +383,24 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.out_img = out_img;
     a.partials = partials.get<float>();
     a.partial_loss = ploss.get<double>();
+    a.pstate = pstate.get<drh::PixState>();
+    a.tl_k = tk.get<uint32_t>();
+    a.tl_on = ton.get<uint64_t>();
+    a.tl_band = tband.get<uint64_t>();
+    a.tl_n = tn.get<int>();
+    a.grads = out_grads;
+    a.losses = out_losses;
+    a.deterministic = det ? 1 : 0;
     {
         KernelTimer kt(ctx, TK_RASTER, s);
-        HIP_TRY(drh::launch_raster(mode, fast, a, s), "raster_kernel launch");
+        HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
     }
     if (mode != drh::MODE_RENDER) {
+        {
+            KernelTimer kt(ctx, TK_BACKWARD, s);
+            HIP_TRY(drh::launch_backward(mode, fast, a, s), "backward_kernel launch");
+        }
+        if (!det) return DRH_OK;
         KernelTimer kt(ctx, TK_REDUCE, s);
         HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3 * H * W, out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s),
@@ -464,8 +491,8 @@ int drh_timing_read(drh_ctx* ctx, drh_timings* out) {
         std::lock_guard<std::mutex> g(ctx->mu);
         launches.swap(ctx->pending);
     }
-    double ms[TK_COUNT] = {0, 0, 0, 0};
-    int64_t n[TK_COUNT] = {0, 0, 0, 0};
+    double ms[TK_COUNT] = {};
+    int64_t n[TK_COUNT] = {};
     int rc = DRH_OK;
     for (auto& l : launches) {
         float t = 0.0f;
@@ -487,6 +514,8 @@ int drh_timing_read(drh_ctx* ctx, drh_timings* out) {
     out->raster_n = n[TK_RASTER];
     out->reduce_n = n[TK_REDUCE];
     out->adam_n = n[TK_ADAM];
+    out->backward_ms = ms[TK_BACKWARD];
+    out->backward_n = n[TK_BACKWARD];
     return rc;
 }
 
@@ -670,8 +699,10 @@ int drh_fit(drh_ctx* ctx, const float* target, int64_t H, int64_t W, const float
     drh::FitState probe{};
     for (int64_t i = 0; i < (int64_t)iters; i++) {
         float sigma = sigma_at(cfg, i);
+        // Fixed-order gradient sums: a fit with a given start is reproducible,
+        // as the reference's is (fit.rs:487-496).
         if ((rc = run_raster(ctx, drh::MODE_LOSS, d_params, bg.dev, tg.dev, 1, (int)T, (int)H, (int)W, sigma,
-                             nullptr, d_grads, d_loss, flags, s)))
+                             nullptr, d_grads, d_loss, flags | DRH_DETERMINISTIC, s)))
             return rc;
         int32_t t = (int32_t)(i + 1);
         float bc1 = 1.0f - powi_f32(beta1, t), bc2 = 1.0f - powi_f32(beta2, t);

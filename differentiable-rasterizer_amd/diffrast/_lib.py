@@ -28,6 +28,7 @@ ERR_NAMES = {
 HOST_PTRS = 0x1
 SYNC = 0x2
 EXACT_MATH = 0x4
+DETERMINISTIC = 0x8
 
 STOP_REASONS = {0: "Completed", 1: "Converged", 2: "Diverged"}
 CONFIG_ERRORS = {1: "NoTriangles", 2: "NonPositiveSigma", 3: "SigmaNotDecreasing",
@@ -79,6 +80,8 @@ class Timings(ctypes.Structure):
         ("raster_n", ctypes.c_int64),
         ("reduce_n", ctypes.c_int64),
         ("adam_n", ctypes.c_int64),
+        ("backward_ms", ctypes.c_double),
+        ("backward_n", ctypes.c_int64),
     ]
 
 
@@ -225,7 +228,7 @@ class Context:
         return out
 
     def fused_loss_backward(self, params, targets, sigma: float, background=(0, 0, 0),
-                            exact: bool = False, want_images: bool = False):
+                            exact: bool = False, want_images: bool = False, deterministic: bool = False):
         p, t = _f32(params), _f32(targets)
         B, T = p.shape[0], p.shape[1]
         H, W = t.shape[1], t.shape[2]
@@ -234,18 +237,20 @@ class Context:
         grads = np.empty((B, T, 10), np.float32)
         imgs = np.empty((B, H, W, 3), np.float32) if want_images else None
         self.fused_ptr(_ptr(p), _ptr(bgs), _ptr(t), B, T, H, W, sigma, _ptr(losses), _ptr(grads),
-                       _ptr(imgs), flags=HOST_PTRS | (EXACT_MATH if exact else 0))
+                       _ptr(imgs), flags=HOST_PTRS | (EXACT_MATH if exact else 0) |
+                       (DETERMINISTIC if deterministic else 0))
         return (losses, grads, imgs) if want_images else (losses, grads)
 
     def backward_from_grad(self, params, grad_images, sigma: float, background=(0, 0, 0),
-                           exact: bool = False) -> np.ndarray:
+                           exact: bool = False, deterministic: bool = False) -> np.ndarray:
         p, g = _f32(params), _f32(grad_images)
         B, T = p.shape[0], p.shape[1]
         H, W = g.shape[1], g.shape[2]
         bgs = _bgs(background, B)
         grads = np.zeros((B, T, 10), np.float32)
         self.from_grad_ptr(_ptr(p), _ptr(bgs), _ptr(g), B, T, H, W, sigma, _ptr(grads),
-                           flags=HOST_PTRS | (EXACT_MATH if exact else 0))
+                           flags=HOST_PTRS | (EXACT_MATH if exact else 0) |
+                           (DETERMINISTIC if deterministic else 0))
         return grads
 
     def adam_project_step(self, params: np.ndarray, grads, m: np.ndarray, v: np.ndarray, lr,

@@ -48,6 +48,8 @@ enum {
 #define DRH_HOST_PTRS 0x1u  /* array arguments are host memory */
 #define DRH_SYNC 0x2u       /* with device pointers: wait for the stream before returning */
 #define DRH_EXACT_MATH 0x4u /* IEEE division, sqrt and expf in the per-pixel geometry */
+#define DRH_DETERMINISTIC 0x8u /* gradients summed in a fixed order: bit-identical run to run
+                                  (default: one float atomic per triangle parameter per block) */
 
 /* Bounded host wait, as GpuRasterizer::POLL_TIMEOUT (crates/diffrast-gpu/src/lib.rs:229). */
 #define DRH_WAIT_TIMEOUT_S 60
@@ -85,8 +87,10 @@ int drh_clear_pool(drh_ctx *ctx);
  * milliseconds and launch counts since the last read, and resets them. The
  * events do not synchronize the host between kernels. */
 typedef struct {
-    double setup_ms, raster_ms, reduce_ms, adam_ms;
+    double setup_ms, raster_ms, reduce_ms, adam_ms;  /* raster: the forward kernel */
     int64_t setup_n, raster_n, reduce_n, adam_n;
+    double backward_ms;                              /* the backward kernel */
+    int64_t backward_n;
 } drh_timings;
 
 int drh_timing_enable(drh_ctx *ctx, int enable);

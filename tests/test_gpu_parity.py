@@ -199,12 +199,26 @@ def test_gradient_input_mode_matches_target_mode(ctx):  # crates/diffrast-gpu/sr
     assert grad_err(g_g, g_t) <= 1e-6
 
 
-def test_results_are_bit_reproducible(ctx):
+def test_results_are_bit_reproducible(ctx, orc):
+    # DRH_DETERMINISTIC: per-block partial rows summed in a fixed order.
     params = synth.batch("uniform", 4, 128, 15)
     targets = np.stack([synth.blob_target(30 + b, 96, 96) for b in range(4)])
-    a = ctx.fused_loss_backward(params, targets, 0.0015)
-    b = ctx.fused_loss_backward(params, targets, 0.0015)
+    a = ctx.fused_loss_backward(params, targets, 0.0015, deterministic=True)
+    b = ctx.fused_loss_backward(params, targets, 0.0015, deterministic=True)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    # the default (one float atomic per triangle parameter per block) agrees
+    # with it, and with the oracle, to the gradient bar
+    c = ctx.fused_loss_backward(params, targets, 0.0015)
+    assert np.array_equal(a[0], c[0])
+    assert grad_err(c[1], a[1]) <= 1e-6
+    cl, cg = orc.loss_backward_batch(params, targets, 0.0015)
+    check_losses(a[0], cl)
+    assert grad_err(a[1], cg) <= GRAD_RTOL
+    gin = ((synth.uniforms(6, 4 * 96 * 96 * 3) - 0.5) * 1e-3).reshape(4, 96, 96, 3).astype(np.float32)
+    d1 = ctx.backward_from_grad(params, gin, 0.0015, deterministic=True)
+    d2 = ctx.backward_from_grad(params, gin, 0.0015, deterministic=True)
+    assert np.array_equal(d1, d2)
+    assert grad_err(ctx.backward_from_grad(params, gin, 0.0015), d1) <= 1e-6
 
 
 def test_pool_reuses_buffers_across_identical_calls(ctx):  # crates/diffrast-gpu/src/lib.rs:1420-1476
@@ -215,7 +229,11 @@ def test_pool_reuses_buffers_across_identical_calls(ctx):  # crates/diffrast-gpu
     second = ctx.fused_loss_backward(params, targets, 0.02)
     s2 = ctx.pool_stats()
     assert s2["misses"] == s1["misses"] and s2["hits"] > s1["hits"]
-    assert np.array_equal(first[0], second[0]) and np.array_equal(first[1], second[1])
+    # reused buffers give the same results: to the reference's bar
+    # (crates/diffrast-gpu/src/lib.rs:1479-1484), as float atomics may sum in
+    # another order; the losses are summed in a fixed order either way
+    assert np.array_equal(first[0], second[0])
+    assert grad_err(second[1], first[1]) <= 1e-4
     ctx.clear_pool()
     assert ctx.pool_stats()["bytes"] == 0
 
