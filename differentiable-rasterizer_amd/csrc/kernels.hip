@@ -305,6 +305,8 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
 // tile and the other two edge lines stay clear of it, so the signs of their
 // cross products are the same at every pixel (inner side when PLAN_INNER).
 enum : uint32_t { PLAN_GENERAL = 3, PLAN_INNER = 4 };
+// Entry bit: the tile lies inside the triangle's box (no per-pixel box test).
+enum : uint32_t { ENT_INBOX = 0x20 };
 
 // geometry<true> for a single-edge plan: the reference's distance to edge j
 // and its cross product, with the other edges' results known. The excluded
@@ -458,7 +460,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
     int count = 0;
     for (int base = k0; base < k1; base += 64) {
         int k = base + lane;
-        uint32_t cls = 0, plan = PLAN_GENERAL;
+        uint32_t cls = 0, plan = PLAN_GENERAL, extra = 0;
         if (k < k1) {
             const float* r = rec + (size_t)k * REC;
             const int* ri = reinterpret_cast<const int*>(r);
@@ -466,6 +468,8 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
             int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
             if ((flags & F_LIVE) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1) {
                 cls = CLS_PARTIAL;
+                const bool in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
+                if (in_box) extra |= ENT_INBOX;
                 if (flags & F_FAST) {
                     float far = r[R_FAR], deep = r[R_DEEP];
                     float lmin[3], lmax[3];
@@ -481,7 +485,6 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                         culled = culled || (lmin[j] > far);
                         all_deep = all_deep && (lmax[j] < deep);
                     }
-                    bool in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
                     if (culled) {
                         cls = 0;
                     } else if (all_deep && in_box) {
@@ -533,7 +536,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
         if (cls != 0) {
             int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = ((uint32_t)(k - k0) << 8) | (plan << 2) | cls;
+            list[pos] = ((uint32_t)(k - k0) << 8) | extra | (plan << 2) | cls;
         }
         count += (int)__popcll(mask);
     }
@@ -542,37 +545,36 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
 
 // Per-pixel weight of one triangle: returns false when the pair is skipped
 // (outside the box, classified far outside, or w <= MIN_WEIGHT). `band` tells
-// whether the exact path ran, and then `g` holds its geometry.
+// whether the exact path ran, and then `g` holds its geometry. The tests are
+// predicates rather than branches; only the exact path is a (divergent)
+// branch, so the wave runs it once for the lanes that need it.
 template <bool FAST>
 __device__ inline bool pair_weight(const Rec& r, uint32_t ent, int x, int y, Pix p, bool valid, float& w,
                                    float& cov, bool& band, Geo& g, float rsig, float sig) {
-    const bool full = (ent & 3u) == CLS_FULL;
-    band = false;
-    if (!valid) return false;
     const float alpha = r.f(R_A);
-    if (full) {
-        cov = 1.0f;
+    cov = 1.0f;
+    if ((ent & 3u) == CLS_FULL) {
+        band = false;
         w = alpha;
-        return !(w <= MIN_WEIGHT);
+        return valid && !(w <= MIN_WEIGHT);
     }
-    if (!(x >= r.i(R_BOX) && x < r.i(R_BOX + 2) && y >= r.i(R_BOX + 1) && y < r.i(R_BOX + 3))) return false;
+    bool act = valid;
+    if (!(ent & ENT_INBOX))
+        act = act && (unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX)) &&
+              (unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1));
+    band = act;
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
         // Conservative classification by the outward edge-line distances.
         float l0 = fmaf(p.px, r.f(R_N + 0), fmaf(p.py, r.f(R_N + 1), -r.f(R_OFF + 0)));
         float l1 = fmaf(p.px, r.f(R_N + 2), fmaf(p.py, r.f(R_N + 3), -r.f(R_OFF + 1)));
         float l2 = fmaf(p.px, r.f(R_N + 4), fmaf(p.py, r.f(R_N + 5), -r.f(R_OFF + 2)));
         float lm = fmaxf(fmaxf(l0, l1), l2);
-        if (lm > r.f(R_FAR)) return false;
-        if (lm < r.f(R_DEEP)) {
-            cov = 1.0f;
-            w = alpha;
-            return !(w <= MIN_WEIGHT);
-        }
+        act = act && !(lm > r.f(R_FAR));
+        band = act && !(lm < r.f(R_DEEP));
     }
-    exact_cov<FAST>(r, p, (ent >> 2) & 7u, rsig, sig, g, cov);
+    if (band) exact_cov<FAST>(r, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
-    band = true;
-    return !(w <= MIN_WEIGHT);
+    return act && !(w <= MIN_WEIGHT);
 }
 
 struct Trans {
@@ -582,22 +584,18 @@ struct Trans {
 };
 
 __device__ inline void trans_mul(Trans& t, float f) {
-    if (f == 0.0f) {
-        t.z += 1;
-    } else {
-        t.q *= f;
-        if (t.q < 5.421010862427522e-20f) {  // 2^-64
-            t.q *= 1.8446744073709552e19f;   // 2^64
-            t.e += 1;
-        }
-    }
+    const bool zero = f == 0.0f;
+    float q = zero ? t.q : t.q * f;
+    const bool small = q < 5.421010862427522e-20f;  // 2^-64
+    t.q = small ? q * 1.8446744073709552e19f : q;   // 2^64
+    t.e += small ? 1 : 0;
+    t.z += zero ? 1 : 0;
 }
 
 // prod_{j>k} (1 - w_j) from the totals and the prefix through k.
 __device__ inline float trans_suffix(const Trans& total, const Trans& prefix) {
-    if (total.z != prefix.z) return 0.0f;
-    float ratio = total.q * __builtin_amdgcn_rcpf(prefix.q);
-    return ldexpf(ratio, -64 * (total.e - prefix.e));
+    float ratio = ldexpf(total.q * __builtin_amdgcn_rcpf(prefix.q), -64 * (total.e - prefix.e));
+    return total.z != prefix.z ? 0.0f : ratio;
 }
 
 // Tile geometry shared by both kernels: one wave per 8x8 tile, four tiles
@@ -680,10 +678,14 @@ __global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const
             bool band;
             Geo g;
             bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
-            if (on) {
-                float omw = 1.0f - w;
-                for (int ch = 0; ch < 3; ch++) col[ch] = r.f(R_C + ch) * w + col[ch] * omw;
-                if (MODE != MODE_RENDER) trans_mul(tot, omw);
+            {
+                // raster.rs:60-66, kept only where the pair contributes
+                const float omw = 1.0f - w;
+                for (int ch = 0; ch < 3; ch++) {
+                    const float o = r.f(R_C + ch) * w + col[ch] * omw;
+                    col[ch] = on ? o : col[ch];
+                }
+                if (MODE != MODE_RENDER) trans_mul(tot, on ? omw : 1.0f);
             }
             if (MODE != MODE_RENDER) {
                 uint64_t onm = __ballot(on);
@@ -751,23 +753,29 @@ struct Back {
 };
 
 // The backward of one triangle at this lane's pixel (grad.rs:148-181) into the
-// lane's partial gradient `a` (zero where the lane does not contribute).
-__device__ inline void grad_pixel(const Rec& r, bool on, bool band, float w, float cov, const Geo& g, Pix p,
-                                  float rsig, Back& st, float (&a)[NP]) {
-    for (int j = 0; j < NP; j++) a[j] = 0.0f;
-    if (!on) return;
-    float omw = 1.0f - w;
-    trans_mul(st.pre, omw);
-    float tk = trans_suffix(st.tot, st.pre);
-    float d_w = 0.0f;
+// lane's partial gradient `a`, zero where the lane does not contribute. The
+// chain is predicated rather than branched: in the backward every entry has
+// contributing lanes, so a branch would never skip. `any_band` (wave-uniform)
+// skips the vertex terms when no lane took the exact path.
+__device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_band, float w, float cov,
+                                  const Geo& g, Pix p, float rsig, Back& st, float (&a)[NP]) {
+    const float omw = 1.0f - w;
+    trans_mul(st.pre, on ? omw : 1.0f);
+    // d_canvas as the reference holds it at layer k: g0 prod_{j>k} (1 - w_j)
+    const float tk = on ? trans_suffix(st.tot, st.pre) : 0.0f;
+    const float tw = tk * w;
+    float sw = 0.0f;
     for (int ch = 0; ch < 3; ch++) {
-        float gk = st.g0[ch] * tk;  // d_canvas as the reference holds it at layer k
-        a[6 + ch] = gk * w;
-        d_w = fmaf(gk, r.f(R_C + ch) - st.col[ch], d_w);
-        st.col[ch] = r.f(R_C + ch) * w + st.col[ch] * omw;
+        a[6 + ch] = st.g0[ch] * tw;
+        sw = fmaf(st.g0[ch], r.f(R_C + ch) - st.col[ch], sw);
+        const float o = fmaf(r.f(R_C + ch), w, st.col[ch] * omw);
+        st.col[ch] = on ? o : st.col[ch];
     }
-    if (r.i(R_FLAGS) & F_ACTIVE) a[9] = d_w * cov;
-    float d_cov = d_w * r.f(R_A);
+    const float d_w = tk * sw;
+    a[9] = (r.i(R_FLAGS) & F_ACTIVE) ? d_w * cov : 0.0f;
+    for (int j = 0; j < 6; j++) a[j] = 0.0f;
+    if (!any_band) return;
+    const float d_cov = d_w * r.f(R_A);
     // grad.rs:252-268: vertex terms, zero exactly on the boundary.
     if (band && g.dist >= 1e-9f) {
         // u = (pt - cp) / dist with cp = a + t (b - a), rounded as
@@ -777,8 +785,8 @@ __device__ inline void grad_pixel(const Rec& r, bool on, bool band, float w, flo
         float inv = __builtin_amdgcn_rcpf(g.dist);
         float cpx = g.ax + g.t * g.ex, cpy = g.ay + g.t * g.ey;
         float ux = (p.px - cpx) * inv, uy = (p.py - cpy) * inv;
-        float sgn = g.sd > 0.0f ? 1.0f : -1.0f;
-        float chain = d_cov * cov * (1.0f - cov) * rsig * sgn;
+        float chain = d_cov * cov * (1.0f - cov) * rsig;
+        chain = g.sd > 0.0f ? chain : -chain;
         float A = -(1.0f - g.t) * chain;  // onto the edge's first vertex
         float Bc = -g.t * chain;           // onto its second vertex
         float s0 = g.edge == 0 ? A : (g.edge == 2 ? Bc : 0.0f);
@@ -874,19 +882,12 @@ __global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, cons
                 const bool on = (onm >> lane) & 1u;
                 const bool band = (bm >> lane) & 1u;
                 const Rec r = load_rec(rec + (size_t)k * REC);
-                float w = 0.0f, cov = 0.0f;
+                float cov = 1.0f;
                 Geo g;
-                if (on) {
-                    if (band) {
-                        exact_cov<FAST>(r, tg.p, (e2 >> 2) & 7u, rsig, sig, g, cov);
-                        w = r.f(R_A) * cov;
-                    } else {
-                        cov = 1.0f;
-                        w = r.f(R_A);
-                    }
-                }
+                if (band) exact_cov<FAST>(r, tg.p, (e2 >> 2) & 7u, rsig, sig, g, cov);
+                const float w = r.f(R_A) * cov;
                 float part[NP];
-                grad_pixel(r, on, band, w, cov, g, tg.p, rsig, st, part);
+                grad_pixel(r, on, band, bm != 0, w, cov, g, tg.p, rsig, st, part);
                 reduce_entry(part, bm != 0, accw + (k - k0) * NP, lane, p10);
             }
         } else {
@@ -904,9 +905,11 @@ __global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, cons
                 Geo g;
                 bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
                 if (__ballot(on) == 0) continue;
+                const bool any_band = __ballot(on && band) != 0;
+                band = band && on;
                 float part[NP];
-                grad_pixel(r, on, band, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, __ballot(on && band) != 0, accw + kl * NP, lane, p10);
+                grad_pixel(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
+                reduce_entry(part, any_band, accw + kl * NP, lane, p10);
             }
         }
         __syncthreads();
