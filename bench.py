@@ -1,17 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark: batched soft-raster forward + MSE + backward on one MI355X.
 
-One step = one drh_fused_loss_backward call (records, fused raster kernel,
-partial-row reduction) over the headline workload: B=16 scenes at 256x256,
+One step = one drh_fused_loss_backward call (setup_records, forward_kernel,
+backward_kernel) over the headline workload: B=16 scenes at 256x256,
 T=128 triangles each, sigma=0.0015, synthetic seeded scenes (diffrast.synth)
 and targets rendered from independently seeded scenes. Inputs and outputs
 stay in HBM; the timed region is K steps between two synchronizations.
 
 Printed (one JSON line on stdout): throughput in dense pixel-triangle
 evaluations per second, ms per batch, the dominant kernel's roofline position
-(algorithmic FLOP per launch over its event-timed average duration, against
-the FP32 vector peak), the CPU baseline (the C oracle, one thread per scene,
-on this host's cores), and side measurements of the other workloads.
+(backward_kernel: its algorithmic FLOP per launch over its event-timed average
+duration, against the FP32 vector peak; the forward kernel and the pair are
+reported beside it), the CPU baseline (the C oracle, one thread per scene, on
+this host's cores), and side measurements of the other workloads.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
     python bench.py --copy-calibration     # plain device copy, for PMC scaling
@@ -45,7 +46,9 @@ SIGMA = 0.0015                # python/diffrast/torch_layer.py:73
 #   coverage evaluation 74 per box pair, once forward and once backward
 #   forward composite 10 per contributing pair, backward chain 51
 #   loss + dL/dpixel 15 per pixel
-FLOP_BOX, FLOP_CONTRIB, FLOP_PIXEL = 148, 61, 15
+# forward_kernel: 74 box + 10 contrib + 15 pixel; backward_kernel: 74 box + 51 contrib
+FLOP_FWD = (74, 10, 15)
+FLOP_BWD = (74, 51, 0)
 
 
 def log(*a):
@@ -105,15 +108,16 @@ def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev):
         t = ctx.read_timings()
     finally:
         ctx.timing(False)
-    return {k: t[f"{k}_ms"] / max(t[f"{k}_n"], 1) for k in ("setup", "raster", "backward", "reduce")}
+    names = {"setup": "setup", "forward": "raster", "backward": "backward", "reduce": "reduce"}
+    return {k: t[f"{f}_ms"] / max(t[f"{f}_n"], 1) for k, f in names.items()}
 
 
-def traffic_from_profiles():
-    """HBM bytes per raster launch from the committed PMC summary, if any."""
-    f = ROOT / "profiles" / "raster_kernel_c2_pmc.md"
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, if any."""
+    f = ROOT / "profiles" / "raster_kernels_c2_pmc.md"
     if not f.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    m = re.search(kernel + r" traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
     return float(m.group(1)) if m else None
 
 
@@ -250,21 +254,32 @@ def main():
         l = losses.cpu().numpy().astype(np.float64)
         loss_rel = float(np.max(np.abs(l - cpu["losses"]) / np.abs(cpu["losses"])))
         out["parity_vs_oracle"] = {"grad_max_abs_over_norm": grad_rel, "loss_rel": loss_rel}
-        flop = FLOP_BOX * cpu["n_box"] + FLOP_CONTRIB * cpu["n_contrib"] + FLOP_PIXEL * B * H * W
-        achieved = flop / (kt["raster"] / 1e3) / 1e12
-        out["roofline"] = {
-            "bound": "valu",
-            "achieved": achieved,
-            "peak": PEAK_FP32_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_TFLOPS,
-            "traffic": traffic_from_profiles(),
-            "kernel": "raster_kernel<MODE_LOSS>",
-            "flop_per_launch": flop,
-            "n_box_pairs": cpu["n_box"],
-            "n_contrib_pairs": cpu["n_contrib"],
-            "frac_nonpacked_peak": achieved / PEAK_FP32_NONPACKED,
-        }
+        counts = (cpu["n_box"], cpu["n_contrib"], B * H * W)
+        flop_f = sum(a * b for a, b in zip(FLOP_FWD, counts))
+        flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
+
+        def roof(kernel, flop, ms_k):
+            achieved = flop / (ms_k / 1e3) / 1e12
+            return {
+                "bound": "valu",
+                "achieved": achieved,
+                "peak": PEAK_FP32_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": achieved / PEAK_FP32_TFLOPS,
+                "traffic": traffic_from_profiles(kernel),
+                "kernel": kernel,
+                "flop_per_launch": flop,
+                "ms_per_launch": ms_k,
+                "frac_nonpacked_peak": achieved / PEAK_FP32_NONPACKED,
+            }
+
+        out["roofline"] = roof("backward_kernel", flop_b, kt["backward"])
+        out["roofline"]["n_box_pairs"] = cpu["n_box"]
+        out["roofline"]["n_contrib_pairs"] = cpu["n_contrib"]
+        out["roofline_forward"] = roof("forward_kernel", flop_f, kt["forward"])
+        both = roof("forward_kernel+backward_kernel", flop_f + flop_b, kt["forward"] + kt["backward"])
+        both["traffic"] = None
+        out["roofline_pair"] = both
         out["cpu_baseline"] = {
             "value": dense / cpu["per_batch_s"],
             "unit": UNIT,

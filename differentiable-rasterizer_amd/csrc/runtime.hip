@@ -67,9 +67,10 @@ constexpr uint64_t POOL_BYTE_LIMIT = 512ull << 20;
 struct PoolBuf {
     void* ptr = nullptr;
     size_t bytes = 0;
-    hipEvent_t ev = nullptr;          // recorded when the last user released it
+    hipEvent_t ev = nullptr;          // recorded when the last user released it (multi-stream)
     hipStream_t stream = nullptr;     // stream of that last use
     bool used = false;
+    bool ev_recorded = false;         // `ev` marks the end of the last use
 };
 
 }  // namespace
@@ -89,6 +90,10 @@ struct drh_ctx {
     std::mutex mu;
     std::unordered_map<uint64_t, std::vector<PoolBuf>> free_bufs;
     uint64_t hits = 0, misses = 0, bytes = 0;
+    // Set once buffers have been used on more than one stream. Until then
+    // every use of a buffer is ordered by the one stream and releases record
+    // no event (an event record costs a GPU-side marker per buffer per call).
+    bool multi_stream = false;
     // kernel timing (drh_timing_enable / drh_timing_read)
     bool timing = false;
     std::vector<TimedLaunch> pending;
@@ -98,9 +103,11 @@ namespace {
 
 uint64_t pool_key(uint64_t kind, size_t bytes) { return (kind << 56) | (uint64_t)bytes; }
 
-// A buffer borrowed from the pool for the duration of one call. On release an
-// event is recorded on the stream, and a later user on a different stream
-// waits for it, so reuse never races queued work.
+// A buffer borrowed from the pool for the duration of one call. Reuse on the
+// stream of the last use is ordered by that stream. Once a context sees a
+// second stream, releases record an event that a user on another stream
+// waits for; at that first switch the device is synchronized once, since the
+// earlier uses recorded none. Either way reuse never races queued work.
 class Lease {
   public:
     Lease() = default;
@@ -125,8 +132,15 @@ class Lease {
         }
         if (buf_.ptr) {
             if (buf_.used && buf_.stream != s) {
-                hipError_t e = hipStreamWaitEvent(s, buf_.ev, 0);
-                if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+                if (buf_.ev_recorded) {
+                    hipError_t e = hipStreamWaitEvent(s, buf_.ev, 0);
+                    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+                } else {
+                    hipError_t e = hipDeviceSynchronize();
+                    if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+                }
+                std::lock_guard<std::mutex> g(ctx->mu);
+                ctx->multi_stream = true;
             }
             return DRH_OK;
         }
@@ -153,7 +167,12 @@ class Lease {
 
     void release() {
         if (!buf_.ptr) return;
-        (void)hipEventRecord(buf_.ev, stream_);
+        bool multi;
+        {
+            std::lock_guard<std::mutex> g(ctx_->mu);
+            multi = ctx_->multi_stream;
+        }
+        buf_.ev_recorded = multi && hipEventRecord(buf_.ev, stream_) == hipSuccess;
         buf_.stream = stream_;
         buf_.used = true;
         bool keep = false;
@@ -166,7 +185,11 @@ class Lease {
             }
         }
         if (!keep) {
-            (void)hipEventSynchronize(buf_.ev);
+            // the queued work that uses the buffer finishes before it is freed
+            if (buf_.ev_recorded)
+                (void)hipEventSynchronize(buf_.ev);
+            else
+                (void)hipStreamSynchronize(stream_);
             (void)hipEventDestroy(buf_.ev);
             (void)hipFree(buf_.ptr);
         }

@@ -113,11 +113,26 @@ _lib = None
 _lock = threading.Lock()
 
 
+def _load_torch_runtime() -> None:
+    """Load PyTorch's HIP runtime first, when PyTorch is installed.
+
+    A process has one libamdhip64.so.7: PyTorch bundles its own and the library
+    links the system one under the same soname, so whichever is loaded first
+    serves both. PyTorch only works with its own, and the torch layer passes
+    its device pointers and streams to this library, so it must come first.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib() -> ctypes.CDLL:
     """Load the HIP library; raises if it has not been built."""
     global _lib
     with _lock:
         if _lib is None:
+            _load_torch_runtime()
             if not LIB_PATH.exists():
                 raise ImportError(
                     f"{LIB_PATH} is missing; build it with `python build.py` "

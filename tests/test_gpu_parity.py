@@ -238,6 +238,35 @@ def test_pool_reuses_buffers_across_identical_calls(ctx):  # crates/diffrast-gpu
     assert ctx.pool_stats()["bytes"] == 0
 
 
+def test_pool_buffers_move_between_streams(ctx):
+    # Pooled buffers used on one stream, then on others (device pointers,
+    # asynchronous calls): results identical to a single-stream run.
+    import torch
+
+    from diffrast import _lib
+
+    dev = torch.device("cuda:0")
+    B, H, W, T, sigma = 2, 40, 48, 20, 0.01
+    params = torch.from_numpy(synth.batch("uniform", B, T, 21)).to(dev)
+    targets = torch.from_numpy(np.stack([synth.blob_target(40 + b, H, W) for b in range(B)])).to(dev)
+    bg = torch.zeros((B, 3), device=dev)
+
+    def run(stream):
+        losses = torch.empty(B, device=dev)
+        grads = torch.empty((B, T, 10), device=dev)
+        ctx.fused_ptr(params.data_ptr(), bg.data_ptr(), targets.data_ptr(), B, T, H, W, sigma,
+                      losses.data_ptr(), grads.data_ptr(), None, stream.cuda_stream, _lib.DETERMINISTIC)
+        return losses, grads
+
+    ref = run(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    outs = [run(s) for s in (s1, s2, s1, s2, torch.cuda.current_stream(dev))]
+    torch.cuda.synchronize()
+    for losses, grads in outs:
+        assert torch.equal(losses, ref[0]) and torch.equal(grads, ref[1])
+
+
 def test_adam_step_is_bit_exact(ctx, orc):  # optim.rs:40-60 + fit.rs:399-424
     n = 150
     p0 = synth.uniform_scene(17, 15).ravel().copy()
