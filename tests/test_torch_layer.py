@@ -1,0 +1,313 @@
+"""The torch drop-in, after the reference's python/test_torch_layer.py.
+
+Same cases and bars. Two deliberate differences, both from this build having
+no CPU backend (the product never runs the oracle): `device="cpu"` raises
+ValueError instead of running a CPU path, and "the GPU agrees with the CPU
+but is not bit-identical" compares the HIP path with the oracle.
+
+Argument validation, the dispatch-policy tables and the helpers need no GPU
+and run in the CPU suite; everything that renders is marked `gpu`.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from diffrast.torch_layer import (
+    N_PARAMS,
+    clamp_params,
+    fused_loss,
+    fused_mse,
+    gpu_adapter,
+    last_device,
+    policy_prefers_gpu,
+    psnr,
+    random_params,
+    rasterize,
+)
+
+gpu = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- rasterize
+
+
+@gpu
+def test_output_shape_and_layout():  # test_torch_layer.py:39-44
+    p = random_params(3, 8, generator=_gen(0))
+    assert rasterize(p, 16, 24).shape == (3, 3, 16, 24)
+    assert rasterize(p, 16, 24, channels_first=False).shape == (3, 16, 24, 3)
+    assert rasterize(p.cuda(), 16, 24).device.type == "cuda"
+
+
+@gpu
+def test_render_is_differentiable():  # test_torch_layer.py:46-54
+    p = random_params(1, 4, generator=_gen(0)).requires_grad_(True)
+    rasterize(p, 16, 16, sigma=0.03).sum().backward()
+    assert p.grad is not None and p.grad.shape == p.shape
+    assert torch.isfinite(p.grad).all()
+    assert p.grad.abs().sum() > 0
+
+
+@gpu
+def test_gradient_matches_numerical_differentiation():  # test_torch_layer.py:56-90
+    # eps = 5e-4 sits at the bottom of the finite-difference error curve for
+    # this loss scale (README.md:226-235).
+    eps, sigma = 5e-4, 0.03
+    p = random_params(1, 5, generator=_gen(0)).requires_grad_(True)
+    target = torch.rand(1, 3, 24, 24, generator=_gen(1))
+    F.mse_loss(rasterize(p, 24, 24, sigma=sigma), target).backward()
+    analytic = p.grad.clone()
+
+    numeric = torch.zeros_like(p)
+    flat = numeric.view(-1)
+    with torch.no_grad():
+        base = p.detach().clone()
+        for i in range(base.numel()):
+            for sign in (1, -1):
+                probe = base.clone().view(-1)
+                probe[i] += sign * eps
+                flat[i] += sign * F.mse_loss(rasterize(probe.view_as(base), 24, 24, sigma=sigma), target)
+        flat /= 2 * eps
+
+    rel = ((analytic - numeric).norm() / numeric.norm()).item()
+    cos = F.cosine_similarity(analytic.view(1, -1), numeric.view(1, -1)).item()
+    assert rel < 0.02, f"relative error {rel:.4%}"
+    assert cos > 0.999, f"cosine similarity {cos:.6f}"
+
+
+@gpu
+def test_gradient_descent_reduces_loss():  # test_torch_layer.py:92-113
+    target = rasterize(random_params(1, 6, generator=_gen(3)), 32, 32, sigma=0.002).detach()
+    p = random_params(1, 6, generator=_gen(9)).requires_grad_(True)
+    opt = torch.optim.Adam([p], lr=0.02)
+    first = None
+    for _ in range(60):
+        opt.zero_grad()
+        loss = F.mse_loss(rasterize(p, 32, 32, sigma=0.03), target)
+        loss.backward()
+        opt.step()
+        with torch.no_grad():
+            p.copy_(clamp_params(p))
+        if first is None:
+            first = loss.item()
+    assert loss.item() < first * 0.7, f"loss {first} -> {loss.item()}"
+
+
+@gpu
+def test_gradients_reach_an_upstream_network():  # test_torch_layer.py:115-124
+    torch.manual_seed(0)
+    net = torch.nn.Linear(4, 6 * N_PARAMS)
+    params = net(torch.randn(2, 4)).view(2, 6, N_PARAMS)
+    rasterize(params, 16, 16, sigma=0.03).mean().backward()
+    assert net.weight.grad is not None
+    assert torch.isfinite(net.weight.grad).all() and net.weight.grad.abs().sum() > 0
+
+
+@gpu
+def test_rasterize_routes_to_the_gpu(orc):  # test_torch_layer.py:126-144
+    # Both the forward and the backward must run on the GPU; the backward takes
+    # a different code path. The reference's CPU leg is the oracle here.
+    p = random_params(8, 128, generator=_gen(0)).requires_grad_(True)
+    out = rasterize(p, 64, 64, sigma=0.02, device="gpu")
+    assert last_device() == "gpu"
+    out.sum().backward()
+    assert last_device() == "gpu"
+    ref = orc.backward_from_grad_batch(p.detach().numpy(), np.ones((8, 64, 64, 3), np.float32), 0.02)
+    rel = np.abs(p.grad.numpy() - ref).max() / max(np.linalg.norm(ref), 1e-12)
+    assert rel < 1e-2, f"gpu/oracle gradient gap {rel:.2e}"
+
+
+def test_cpu_device_is_rejected():
+    # No CPU backend in this build: "cpu" fails loudly rather than silently
+    # running something else (the reference runs its Rust CPU path).
+    p = random_params(1, 4, generator=_gen(0))
+    with pytest.raises(ValueError):
+        rasterize(p, 16, 16, device="cpu")
+    with pytest.raises(ValueError):
+        fused_loss(p, torch.rand(1, 16, 16, 3), device="cpu")
+
+
+def test_rejects_bad_shapes_and_sigma():  # test_torch_layer.py:146-153
+    p = random_params(1, 4, generator=_gen(0))
+    with pytest.raises(ValueError):
+        rasterize(p[..., :4], 16, 16)
+    with pytest.raises(ValueError):
+        rasterize(p, 0, 16)
+    with pytest.raises(ValueError):
+        rasterize(p, 16, 16, sigma=0.0)
+
+
+@gpu
+def test_background_is_visible_where_nothing_is_drawn():  # test_torch_layer.py:155-160
+    p = torch.tensor([[[5.0, 5.0, 5.1, 5.0, 5.05, 5.1, 1.0, 1.0, 1.0, 1.0]]])
+    img = rasterize(p, 8, 8, background=(0.25, 0.5, 0.75))
+    assert img[0, 0].mean().item() == pytest.approx(0.25, abs=1e-5)
+    assert img[0, 2].mean().item() == pytest.approx(0.75, abs=1e-5)
+
+
+# ---------------------------------------------------------------- fused_loss
+
+
+@gpu
+def test_fused_loss_matches_autograd_path():  # test_torch_layer.py:165-179
+    p = random_params(2, 5, generator=_gen(0))
+    targets = torch.rand(2, 20, 20, 3, generator=_gen(1))
+    losses, grads = fused_loss(p, targets, sigma=0.03)
+    pg = p.clone().requires_grad_(True)
+    rendered = rasterize(pg, 20, 20, sigma=0.03, channels_first=False)
+    per_item = ((rendered - targets) ** 2).flatten(1).mean(1)
+    per_item.sum().backward()
+    torch.testing.assert_close(losses, per_item.detach(), rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(grads, pg.grad, rtol=1e-3, atol=1e-7)
+
+
+@gpu
+def test_fused_loss_routing_is_honoured():  # test_torch_layer.py:181-198
+    p = random_params(8, 128, generator=_gen(0))
+    targets = torch.rand(8, 64, 64, 3, generator=_gen(1))
+    fused_loss(p, targets, sigma=0.02, device="gpu")
+    assert last_device() == "gpu"
+    fused_loss(p, targets, sigma=0.02, device="auto")
+    assert last_device() == "gpu"
+    assert gpu_adapter() is not None
+
+
+@gpu
+def test_gpu_gradients_agree_with_the_oracle(orc):  # test_torch_layer.py:200-218
+    p = random_params(8, 128, generator=_gen(2))
+    targets = torch.rand(8, 64, 64, 3, generator=_gen(3))
+    gpu_loss, gpu_grads = fused_loss(p, targets, sigma=0.02)
+    cpu_loss, cpu_grads = orc.loss_backward_batch(p.numpy(), targets.numpy(), 0.02)
+    torch.testing.assert_close(gpu_loss, torch.from_numpy(cpu_loss), rtol=1e-4, atol=1e-7)
+    rel = np.abs(gpu_grads.numpy() - cpu_grads).max() / max(np.linalg.norm(cpu_grads), 1e-12)
+    assert rel < 1e-3, f"relative gradient difference {rel:.2e}"
+    # bit-identical would mean the GPU path did not run
+    assert not np.array_equal(gpu_grads.numpy(), cpu_grads)
+
+
+def test_unknown_device_is_rejected():  # test_torch_layer.py:220-224
+    p = random_params(2, 8, generator=_gen(0))
+    with pytest.raises(ValueError):
+        fused_loss(p, torch.rand(2, 16, 16, 3), device="banana")
+
+
+def test_fused_loss_rejects_bad_target_shape():  # test_torch_layer.py:226-229
+    p = random_params(1, 4, generator=_gen(0))
+    with pytest.raises(ValueError):
+        fused_loss(p, torch.rand(1, 3, 8, 8, 1))
+
+
+# ---------------------------------------------------------------- fused_mse
+
+
+@gpu
+def test_fused_mse_matches_rasterize_then_mse():  # test_torch_layer.py:236-261
+    params = random_params(4, 12, generator=_gen(0))
+    target = rasterize(random_params(4, 12, generator=_gen(1)), 32, 32, sigma=0.01).detach()
+    a = params.clone().requires_grad_(True)
+    F.mse_loss(rasterize(a, 32, 32, sigma=0.01), target).backward()
+    b = params.clone().requires_grad_(True)
+    fused = fused_mse(b, target, sigma=0.01)
+    fused.backward()
+    reference = F.mse_loss(rasterize(params, 32, 32, sigma=0.01), target)
+    assert fused.item() == pytest.approx(reference.item(), abs=1e-6)
+    rel = (a.grad - b.grad).abs().max() / a.grad.norm().clamp_min(1e-12)
+    assert rel.item() < 1e-4, f"gradient gap {rel.item():.2e}"
+
+
+@gpu
+def test_fused_mse_on_device_tensors():
+    # Tensors already on the GPU stay there: no host round trip, results on the device.
+    params = random_params(4, 12, generator=_gen(0)).cuda().requires_grad_(True)
+    target = rasterize(random_params(4, 12, generator=_gen(1)).cuda(), 32, 32, sigma=0.01).detach()
+    loss = fused_mse(params, target, sigma=0.01)
+    assert loss.device.type == "cuda"
+    loss.backward()
+    assert params.grad.device.type == "cuda" and torch.isfinite(params.grad).all()
+    host = params.detach().cpu().requires_grad_(True)
+    fused_mse(host, target.cpu(), sigma=0.01).backward()
+    assert torch.allclose(params.grad.cpu(), host.grad, rtol=1e-4, atol=1e-8)
+
+
+@gpu
+def test_gradients_reach_a_network_through_the_fused_loss():  # test_torch_layer.py:263-271
+    torch.manual_seed(0)
+    net = torch.nn.Linear(4, 6 * N_PARAMS)
+    target = torch.rand(2, 3, 16, 16, generator=_gen(2))
+    fused_mse(net(torch.randn(2, 4)).view(2, 6, N_PARAMS), target, sigma=0.02).backward()
+    assert net.weight.grad is not None
+    assert torch.isfinite(net.weight.grad).all() and net.weight.grad.abs().sum() > 0
+
+
+def test_fused_mse_rejects_bad_shapes():  # test_torch_layer.py:273-278
+    p = random_params(2, 4, generator=_gen(0))
+    with pytest.raises(ValueError):
+        fused_mse(p, torch.rand(2, 16, 16, 3))  # channels-last target
+    with pytest.raises(ValueError):
+        fused_mse(p, torch.rand(2, 3, 16, 16), sigma=0.0)
+
+
+# ---------------------------------------------------------------- policy
+# The reference's `device="auto"` rule pinned to its measured crossovers
+# (docs/gpu-report.txt via test_torch_layer.py:281-351): GPU-over-CPU
+# speedups at batch 16; cells within +/-10% are ties and skipped. This build
+# runs "auto" on the GPU whatever the rule says; the rule is kept for callers
+# that query it.
+
+DISCRETE = [
+    (64 * 64, 32, 1.85), (64 * 64, 128, 1.70), (64 * 64, 512, 2.26),
+    (128 * 128, 32, 4.06), (128 * 128, 128, 4.96), (128 * 128, 512, 3.89),
+    (256 * 256, 32, 3.64), (256 * 256, 128, 6.03), (256 * 256, 512, 3.89),
+]
+INTEGRATED = [
+    (64 * 64, 32, 0.60), (64 * 64, 128, 0.43), (64 * 64, 512, 0.43),
+    (128 * 128, 32, 0.51), (128 * 128, 128, 0.39), (128 * 128, 512, 0.34),
+    (256 * 256, 32, 0.31), (256 * 256, 128, 0.33), (256 * 256, 512, 0.35),
+]
+
+
+@pytest.mark.parametrize("discrete,table", [(True, DISCRETE), (False, INTEGRATED)],
+                         ids=["discrete", "integrated"])
+def test_policy_matches_the_crossover_tables(discrete, table):
+    for pixels, tris, speedup in table:
+        if 0.9 <= speedup <= 1.1:
+            continue
+        assert policy_prefers_gpu(16, tris, pixels, discrete) == (speedup > 1.0), (pixels, tris)
+
+
+def test_single_images_and_trivial_workloads_stay_on_the_cpu():  # test_torch_layer.py:331-341
+    assert not policy_prefers_gpu(1, 512, 256 * 256, True)
+    assert policy_prefers_gpu(16, 512, 256 * 256, True)
+    assert not policy_prefers_gpu(4, 8, 16 * 16, True)
+
+
+# ---------------------------------------------------------------- helpers
+
+
+def test_random_params_are_in_range():  # test_torch_layer.py:346-350
+    p = random_params(4, 10, generator=_gen(0))
+    assert p.shape == (4, 10, N_PARAMS)
+    assert (p[..., 6:9] >= 0).all() and (p[..., 6:9] <= 1).all()
+    assert (p[..., 9] > 0).all() and (p[..., 9] < 1).all()
+
+
+def test_clamp_keeps_alpha_off_the_boundary():  # test_torch_layer.py:352-358
+    p = torch.full((1, 1, N_PARAMS), 5.0)
+    p[..., 9] = 1.0
+    out = clamp_params(p)
+    assert 0.0 < out[0, 0, 9].item() < 1.0
+    assert out[0, 0, 0].item() <= 1.25
+
+
+def test_psnr_is_infinite_for_identical_images():  # test_torch_layer.py:360-363
+    a = torch.rand(1, 3, 8, 8, generator=_gen(0))
+    assert torch.isinf(psnr(a, a))
+    assert psnr(a, a * 0.99).item() > 20.0
