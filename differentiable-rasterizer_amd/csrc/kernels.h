@@ -14,7 +14,7 @@ constexpr int CH = 128;   // triangles per chunk (LDS accumulators are per chunk
 // Per-triangle record, REC floats, written by setup_records. The hot loops
 // load fields [0, REC_HOT) of one record per list entry; the rest is read
 // only while building a tile's list.
-constexpr int REC = 52;
+constexpr int REC = 76;
 constexpr int REC_HOT = 40;
 enum RecField : int {
     R_V = 0,       // 6: vertices x0 y0 x1 y1 x2 y2
@@ -34,6 +34,7 @@ enum RecField : int {
     R_D = 40,      // 6: unit edge directions (fast path only)
     R_SOFF = 46,   // 3: a . d per edge
     R_LEN = 49,    // 3: |e|
+    R_EB = 52,     // 3 x 8: per edge a.x a.y e.x e.y |e|^2 1/|e|^2 0 0 (scalar-loaded by edge index)
 };
 // F_CCW: the cross products of inside points are >= 0 (else <= 0).
 enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4, F_CCW = 8 };
@@ -44,6 +45,16 @@ enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2 };
 // kernel (over all chunks); beyond it the backward kernel rebuilds and
 // reclassifies the remaining chunks.
 constexpr int CAP2 = 128;
+
+// One recorded entry of a tile's list, written by the forward kernel and read
+// (with scalar loads) by the backward kernel.
+struct TileEnt {
+    uint32_t k;     // (k << 8) | (plan << 2) | class, k the triangle index
+    uint32_t pad;
+    uint64_t on;    // lanes with w > MIN_WEIGHT
+    uint64_t band;  // of those, lanes on the exact path
+};
+static_assert(sizeof(TileEnt) == 24, "TileEnt is read as 2 + 4 dwords");
 
 // Per-pixel state the forward kernel hands to the backward kernel.
 struct PixState {
@@ -63,9 +74,7 @@ struct RasterArgs {
     float* partials;       // B*nblk*T*NP
     double* partial_loss;  // B*nblk
     PixState* pstate;      // B*H*W
-    uint32_t* tl_k;        // ntiles*CAP2: (k << 8) | (plan << 2) | class
-    uint64_t* tl_on;       // ntiles*CAP2: lanes with w > MIN_WEIGHT
-    uint64_t* tl_band;     // ntiles*CAP2: of those, lanes on the exact path
+    TileEnt* tl_ent;       // ntiles*CAP2 recorded entries
     int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)

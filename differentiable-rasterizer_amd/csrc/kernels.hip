@@ -164,6 +164,15 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
         r[R_D + 2 * j + 1] = dy;
         r[R_SOFF + j] = v[2 * j] * dx + v[2 * j + 1] * dy;
         r[R_LEN + j] = len;
+        float* eb = r + R_EB + 8 * j;
+        eb[0] = v[2 * j];
+        eb[1] = v[2 * j + 1];
+        eb[2] = e[2 * j];
+        eb[3] = e[2 * j + 1];
+        eb[4] = len2[j];
+        eb[5] = rlen2[j];
+        eb[6] = 0.0f;
+        eb[7] = 0.0f;
     }
 }
 
@@ -184,6 +193,18 @@ struct Rec {
 __device__ inline Rec load_rec(const float* __restrict__ r) {
     const f16v* v = reinterpret_cast<const f16v*>(r);
     return Rec{v[0], v[1], *reinterpret_cast<const f8v*>(r + 32)};
+}
+
+// Field i0, i1 or i2 of the record for e = 0, 1, 2. The fields pass through an
+// empty asm that pins them to scalar registers: without it the compiler folds
+// the selects into one variable-index extract from the record vector, which it
+// lowers to a copy of 16 fields into vector registers (uniform e) or a
+// 16-way compare chain (per-lane e). With it, a uniform e becomes s_cselect
+// and a per-lane e two v_cndmask.
+__device__ inline float pick3(const Rec& r, int e, int i0, int i1, int i2) {
+    float f0 = r.f(i0), f1 = r.f(i1), f2 = r.f(i2);
+    asm("" : "+s"(f0), "+s"(f1), "+s"(f2));
+    return e == 0 ? f0 : (e == 1 ? f1 : f2);
 }
 
 struct Pix {
@@ -288,12 +309,11 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
             }
         }
     }
-    // selects rather than a lane-varying index into the (scalar) record
     const int ed = g.edge;
-    g.ax = ed == 0 ? r.f(R_V + 0) : (ed == 1 ? r.f(R_V + 2) : r.f(R_V + 4));
-    g.ay = ed == 0 ? r.f(R_V + 1) : (ed == 1 ? r.f(R_V + 3) : r.f(R_V + 5));
-    g.ex = ed == 0 ? r.f(R_E + 0) : (ed == 1 ? r.f(R_E + 2) : r.f(R_E + 4));
-    g.ey = ed == 0 ? r.f(R_E + 1) : (ed == 1 ? r.f(R_E + 3) : r.f(R_E + 5));
+    g.ax = pick3(r, ed, R_V + 0, R_V + 2, R_V + 4);
+    g.ay = pick3(r, ed, R_V + 1, R_V + 3, R_V + 5);
+    g.ex = pick3(r, ed, R_E + 0, R_E + 2, R_E + 4);
+    g.ey = pick3(r, ed, R_E + 1, R_E + 3, R_E + 5);
     // sqrt is monotone, so sqrt(min d2) == min sqrt(d2) (raster.rs:97-99).
     g.dist = QUICK ? __builtin_amdgcn_sqrtf(best) : sqrtf(best);
     g.sd = inside ? g.dist : -g.dist;
@@ -313,14 +333,12 @@ enum : uint32_t { ENT_INBOX = 0x20 };
 // edges are strictly farther (by a margin well above rounding) at every pixel,
 // so the reference's first-minimum selection picks j with the same distance,
 // and the inside test reduces to the sign of c_j.
-__device__ inline Geo geometry1(const Rec& r, Pix p, uint32_t plan) {
+// The edge's fields come from its block of the record (rp, wave-uniform), one
+// scalar load at an offset set by the plan.
+__device__ inline Geo geometry1(const Rec& r, const float* __restrict__ rp, Pix p, uint32_t plan) {
     const int j = (int)(plan & 3u);
-    const float ax = j == 0 ? r.f(R_V + 0) : (j == 1 ? r.f(R_V + 2) : r.f(R_V + 4));
-    const float ay = j == 0 ? r.f(R_V + 1) : (j == 1 ? r.f(R_V + 3) : r.f(R_V + 5));
-    const float ex = j == 0 ? r.f(R_E + 0) : (j == 1 ? r.f(R_E + 2) : r.f(R_E + 4));
-    const float ey = j == 0 ? r.f(R_E + 1) : (j == 1 ? r.f(R_E + 3) : r.f(R_E + 5));
-    const float len2 = j == 0 ? r.f(R_LEN2 + 0) : (j == 1 ? r.f(R_LEN2 + 1) : r.f(R_LEN2 + 2));
-    const float rl = j == 0 ? r.f(R_RLEN2 + 0) : (j == 1 ? r.f(R_RLEN2 + 1) : r.f(R_RLEN2 + 2));
+    const f8v eb = *reinterpret_cast<const f8v*>(rp + R_EB + 8 * j);
+    const float ax = eb[0], ay = eb[1], ex = eb[2], ey = eb[3], len2 = eb[4], rl = eb[5];
     const float apx = p.px - ax, apy = p.py - ay;
     const float c = ex * apy - ey * apx;
     const float dot = apx * ex + apy * ey;
@@ -331,8 +349,9 @@ __device__ inline Geo geometry1(const Rec& r, Pix p, uint32_t plan) {
     const float dx = apx - g.t * ex;
     const float dy = apy - g.t * ey;
     g.dist = __builtin_amdgcn_sqrtf(dx * dx + dy * dy);
-    const bool ccw = (r.i(R_FLAGS) & F_CCW) != 0;
-    const bool inside = (plan & PLAN_INNER) && (ccw ? c >= 0.0f : c <= 0.0f);
+    // c <= 0 is -c >= 0, also for c = +-0
+    const float cs = (r.i(R_FLAGS) & F_CCW) ? c : -c;
+    const bool inside = (plan & PLAN_INNER) && cs >= 0.0f;
     g.sd = inside ? g.dist : -g.dist;
     g.edge = j;
     g.ax = ax;
@@ -346,10 +365,11 @@ __device__ inline Geo geometry1(const Rec& r, Pix p, uint32_t plan) {
 // and on the plan are wave-uniform; the empty volatile asm keeps the compiler
 // from if-converting them, which would evaluate every variant every time.
 template <bool FAST>
-__device__ inline void exact_cov(const Rec& r, Pix p, uint32_t plan, float rsig, float sig, Geo& g, float& cov) {
+__device__ inline void exact_cov(const Rec& r, const float* __restrict__ rp, Pix p, uint32_t plan, float rsig,
+                                 float sig, Geo& g, float& cov) {
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
         if ((plan & 3u) != PLAN_GENERAL) {
-            g = geometry1(r, p, plan);
+            g = geometry1(r, rp, p, plan);
         } else {
             asm volatile("");
             g = geometry<true>(r, p);
@@ -549,8 +569,8 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
 // predicates rather than branches; only the exact path is a (divergent)
 // branch, so the wave runs it once for the lanes that need it.
 template <bool FAST>
-__device__ inline bool pair_weight(const Rec& r, uint32_t ent, int x, int y, Pix p, bool valid, float& w,
-                                   float& cov, bool& band, Geo& g, float rsig, float sig) {
+__device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, uint32_t ent, int x, int y, Pix p,
+                                   bool valid, float& w, float& cov, bool& band, Geo& g, float rsig, float sig) {
     const float alpha = r.f(R_A);
     cov = 1.0f;
     if ((ent & 3u) == CLS_FULL) {
@@ -572,7 +592,7 @@ __device__ inline bool pair_weight(const Rec& r, uint32_t ent, int x, int y, Pix
         act = act && !(lm > r.f(R_FAR));
         band = act && !(lm < r.f(R_DEEP));
     }
-    if (band) exact_cov<FAST>(r, p, (ent >> 2) & 7u, rsig, sig, g, cov);
+    if (band) exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
     return act && !(w <= MIN_WEIGHT);
 }
@@ -639,8 +659,12 @@ __device__ inline TileGeo tile_geo(int W, int H) {
 // entries that contribute at any of its pixels with their lane masks (on,
 // and exact-path), so the backward kernel neither rebuilds nor reclassifies.
 // MODE_LOSS adds the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114).
+// The waves-per-SIMD floors (8 here, 6 for the backward kernel) cap the
+// register allocation; both kernels wait on scalar loads of the triangle
+// records once per list entry, and the extra waves hide that latency better
+// than the registers they cost would have saved (measured on B=16 256x256).
 template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8))) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ double loss[WAVES];
     const int W = a.W, H = a.H, T = a.T;
@@ -659,9 +683,7 @@ __global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const
     const int n_chunks = (T + CH - 1) / CH;
     int n2 = 0;                 // contributing entries seen (recorded while n2 < CAP2)
     int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
-    uint32_t* tk = a.tl_k + tg.tile * CAP2;
-    uint64_t* ton = a.tl_on + tg.tile * CAP2;
-    uint64_t* tband = a.tl_band + tg.tile * CAP2;
+    TileEnt* te = a.tl_ent + tg.tile * CAP2;
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -673,11 +695,12 @@ __global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const
             const uint32_t ent = uniform_u32(nxt);
             nxt = list[wave][min(i + 1, CH - 1)];
             const int k = k0 + (int)(ent >> 8);
-            const Rec r = load_rec(rec + (size_t)k * REC);
+            const float* rp = rec + (size_t)k * REC;
+            const Rec r = load_rec(rp);
             float w = 0.0f, cov;
             bool band;
             Geo g;
-            bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+            bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
             {
                 // raster.rs:60-66, kept only where the pair contributes
                 const float omw = 1.0f - w;
@@ -690,11 +713,14 @@ __global__ __launch_bounds__(WAVES * 64) void forward_kernel(RasterArgs a, const
             if (MODE != MODE_RENDER) {
                 uint64_t onm = __ballot(on);
                 if (onm != 0) {
-                    uint64_t bm = __ballot(on && band);
+                    const uint64_t bm = __ballot(on && band);
                     if (n2 < CAP2 && lane == 0) {
-                        tk[n2] = ((uint32_t)k << 8) | (ent & 0xFFu);
-                        ton[n2] = onm;
-                        tband[n2] = bm;
+                        TileEnt e;
+                        e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
+                        e.pad = 0;
+                        e.on = onm;
+                        e.band = bm;
+                        te[n2] = e;
                     }
                     n2++;
                 }
@@ -822,7 +848,8 @@ __device__ inline void reduce_entry(const float (&a)[NP], bool any_band, float* 
 // gradients are wave-reduced, accumulated per wave in LDS and written as one
 // partial row per block and chunk.
 template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, const float* __restrict__ records) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(6))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
+                                                               const TileEnt* __restrict__ ents) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
@@ -848,9 +875,8 @@ __global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, cons
     const int n_chunks = (T + CH - 1) / CH;
     const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
     const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
-    const uint32_t* tk = a.tl_k + tg.tile * CAP2;
-    const uint64_t* ton = a.tl_on + tg.tile * CAP2;
-    const uint64_t* tband = a.tl_band + tg.tile * CAP2;
+    // wave-uniform, so the recorded entries are read with scalar loads
+    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * CAP2;
     const size_t blk = tg.tile / WAVES;
     float* accw = acc[wave];
     const int p10 = red10_param(lane);
@@ -868,27 +894,23 @@ __global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, cons
             // The entries the forward kernel recorded: which lanes contribute
             // and which of them took the exact path are known; only w is
             // recomputed. The next entry is read one iteration ahead.
-            uint32_t nk2 = tk[min(i2, CAP2 - 1)];
-            uint64_t non = ton[min(i2, CAP2 - 1)], nbm = tband[min(i2, CAP2 - 1)];
+            TileEnt nx = te[min(i2, CAP2 - 1)];
             for (; i2 < n2r; i2++) {
-                const uint32_t e2 = uniform_u32(nk2);
-                const int k = (int)(e2 >> 8);
+                const TileEnt cur = nx;
+                const int k = (int)(cur.k >> 8);
                 if (k >= k1) break;
-                const uint64_t onm = uniform_u64(non), bm = uniform_u64(nbm);
-                const int i3 = min(i2 + 1, CAP2 - 1);
-                nk2 = tk[i3];
-                non = ton[i3];
-                nbm = tband[i3];
-                const bool on = (onm >> lane) & 1u;
-                const bool band = (bm >> lane) & 1u;
-                const Rec r = load_rec(rec + (size_t)k * REC);
+                nx = te[min(i2 + 1, CAP2 - 1)];
+                const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
+                const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
+                const float* rp = rec + (size_t)k * REC;
+                const Rec r = load_rec(rp);
                 float cov = 1.0f;
                 Geo g;
-                if (band) exact_cov<FAST>(r, tg.p, (e2 >> 2) & 7u, rsig, sig, g, cov);
+                if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
                 const float w = r.f(R_A) * cov;
                 float part[NP];
-                grad_pixel(r, on, band, bm != 0, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, bm != 0, accw + (k - k0) * NP, lane, p10);
+                grad_pixel(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
+                reduce_entry(part, cur.band != 0, accw + (k - k0) * NP, lane, p10);
             }
         } else {
             // Fallback when the forward kernel ran out of record space: rebuild
@@ -899,11 +921,12 @@ __global__ __launch_bounds__(WAVES * 64) void backward_kernel(RasterArgs a, cons
             for (int i = 0; i < count; i++) {
                 const uint32_t ent = uniform_u32(list[wave][i]);
                 const int kl = (int)(ent >> 8);
-                const Rec r = load_rec(rec + (size_t)(k0 + kl) * REC);
+                const float* rp = rec + (size_t)(k0 + kl) * REC;
+                const Rec r = load_rec(rp);
                 float w = 0.0f, cov = 0.0f;
                 bool band = false;
                 Geo g;
-                bool on = pair_weight<FAST>(r, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+                bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
                 if (__ballot(on) == 0) continue;
                 const bool any_band = __ballot(on && band) != 0;
                 band = band && on;
@@ -1102,7 +1125,8 @@ static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
 
 template <int MODE, bool FAST>
 static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((backward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
+    hipLaunchKernelGGL((backward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec,
+                       a.tl_ent);
     return hipGetLastError();
 }
 

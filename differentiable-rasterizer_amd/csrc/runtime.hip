@@ -54,9 +54,7 @@ enum Kind : uint64_t {
     K_FIT_F32,
     K_FIT_STATE,
     K_PIXSTATE,
-    K_TILE_K,
-    K_TILE_ON,
-    K_TILE_BAND,
+    K_TILE_ENT,
     K_TILE_N,
 };
 
@@ -374,7 +372,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     dim3 grid = drh::raster_grid(B, W, H);
     int nblk = (int)(grid.x * grid.y);
     size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pstate, tk, ton, tband, tn;
+    Lease rec, partials, ploss, pstate, tent, tn;
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
     if (mode != drh::MODE_RENDER) {
@@ -382,9 +380,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
             return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
         if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
-        if ((rc = tk.acquire(ctx, K_TILE_K, ntiles * drh::CAP2 * sizeof(uint32_t), s))) return rc;
-        if ((rc = ton.acquire(ctx, K_TILE_ON, ntiles * drh::CAP2 * sizeof(uint64_t), s))) return rc;
-        if ((rc = tband.acquire(ctx, K_TILE_BAND, ntiles * drh::CAP2 * sizeof(uint64_t), s))) return rc;
+        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * drh::CAP2 * sizeof(drh::TileEnt), s))) return rc;
         if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
     }
     {
@@ -407,9 +403,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.partials = partials.get<float>();
     a.partial_loss = ploss.get<double>();
     a.pstate = pstate.get<drh::PixState>();
-    a.tl_k = tk.get<uint32_t>();
-    a.tl_on = ton.get<uint64_t>();
-    a.tl_band = tband.get<uint64_t>();
+    a.tl_ent = tent.get<drh::TileEnt>();
     a.tl_n = tn.get<int>();
     a.grads = out_grads;
     a.losses = out_losses;
