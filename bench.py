@@ -176,6 +176,65 @@ def torch_op_ms(torch, cfg, p, targets, dev, steps=10):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def forward_side(torch, ctx, dev, cpu=True):
+    """Forward-only renders (drh_render): the reference's GPU forward benchmark cells, one
+    Scene::random-shaped scene each at sigma 0.0015 (gpu_bench.rs:18-69), the fit binary's
+    1024-pixel export (fit.rs:95-99), and the c2 batch rendered without gradients. Device
+    time with params and image in HBM; `host_ms` adds the copies in and out (the
+    reference's `render` returns a host canvas)."""
+    from diffrast import synth
+
+    cells = [("fwd_128_T64", 1, 128, 128, 64, 0.0015, "random", 11),
+             ("fwd_256_T128", 1, 256, 256, 128, 0.0015, "random", 11),
+             ("fwd_512_T256", 1, 512, 512, 256, 0.0015, "random", 11),
+             ("fwd_512_T1024", 1, 512, 512, 1024, 0.0015, "random", 11),
+             ("export_1024_T150", 1, 1024, 1024, 150, 0.0015 * 176 / 1024, "export", 12),
+             ("fwd_c2_B16_256_T128", 16, 256, 256, 128, 0.0015, "uniform", 1)]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    for name, B, H, W, T, sig, kind, seed in cells:
+        if kind == "export":
+            params = synth.random_scene(seed, T, 0.18)[None]
+        elif kind == "random":
+            params = synth.random_scene(seed, T)[None]
+        else:
+            params = synth.batch(kind, B, T, seed)
+        bg = np.tile(np.array([[0.1, 0.11, 0.14]], np.float32), (B, 1))
+        p = torch.from_numpy(params).to(dev)
+        b = torch.from_numpy(bg).to(dev)
+        out = torch.empty((B, H, W, 3), device=dev)
+
+        def run():
+            ctx.render_ptr(p.data_ptr(), b.data_ptr(), B, T, H, W, sig, out.data_ptr(), stream)
+
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        n = 20
+        t0 = time.perf_counter()
+        for _ in range(n):
+            run()
+        torch.cuda.synchronize()
+        dev_ms = (time.perf_counter() - t0) * 1e3 / n
+        for _ in range(2):
+            ctx.render(params, H, W, sig, bg)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            ctx.render(params, H, W, sig, bg)
+        host_ms = (time.perf_counter() - t0) * 1e3 / 5
+        res[name] = {"B": B, "H": H, "W": W, "T": T, "sigma": sig, "ms": round(dev_ms, 4),
+                     "host_ms": round(host_ms, 4), "pixel_tri_per_s": B * H * W * T / (dev_ms / 1e3)}
+        if cpu and name == "fwd_512_T1024":
+            from oracle import oracle
+
+            t0 = time.perf_counter()
+            oracle.render_batch(params, H, W, sig, bg, nthreads=1)
+            cpu_ms = (time.perf_counter() - t0) * 1e3
+            res[name]["cpu_oracle_1thread_ms"] = round(cpu_ms, 2)
+            res[name]["speedup_vs_cpu_1thread"] = round(cpu_ms / dev_ms, 1)
+    return res
+
+
 def copy_calibration(torch):
     """A plain device copy of known size: the scale for FETCH_SIZE/WRITE_SIZE."""
     n = 64 << 20  # floats (256 MiB)
@@ -305,6 +364,7 @@ def main():
                           "pixel_tri_per_s": c["B"] * c["H"] * c["W"] * c["T"] / (m / 1e3)}
         side["c4_fit_800_iters"] = fit_side(ctx)
         side["c2_torch_fused_mse_fwd_bwd_ms"] = round(torch_op_ms(torch, cfg, p, targets, dev), 4)
+        side["forward_only"] = forward_side(torch, ctx, dev, cpu=not args.no_cpu_baseline)
         out["side"] = side
 
     print(json.dumps(out), flush=True)

@@ -78,9 +78,25 @@ def small_scene(seed: int, T: int, spread: float = 0.05) -> np.ndarray:
     return out
 
 
+def random_scene(seed: int, T: int, seed_scale: float = 0.15) -> np.ndarray:
+    """(T, 10) scene shaped like the reference's `Scene::random` (scene.rs:58-76): per
+    triangle a centre U[0,1)^2, three vertices centre + U[-s, s)^2, rgb U[0,1), alpha
+    U[0.3,0.8). Same distributions, our own generator (the reference draws from StdRng)."""
+    u = uniforms(seed, T * 12).reshape(T, 12)
+    out = np.empty((T, 10), np.float32)
+    cx, cy = u[:, 0].astype(np.float32), u[:, 1].astype(np.float32)
+    s = np.float32(seed_scale)
+    for v in range(3):
+        out[:, 2 * v] = cx + _rng_range(u[:, 2 + 2 * v], -s, s)
+        out[:, 2 * v + 1] = cy + _rng_range(u[:, 3 + 2 * v], -s, s)
+    out[:, 6:9] = u[:, 8:11].astype(np.float32)
+    out[:, 9] = _rng_range(u[:, 11], 0.3, 0.8)
+    return out
+
+
 def batch(kind: str, B: int, T: int, seed: int, target_offset: int = 0) -> np.ndarray:
     """(B, T, 10) with item b drawn from seed + target_offset + b."""
-    fn = {"uniform": uniform_scene, "small": small_scene}[kind]
+    fn = {"uniform": uniform_scene, "small": small_scene, "random": random_scene}[kind]
     return np.stack([fn(seed + target_offset + b, T) for b in range(B)])
 
 
