@@ -103,6 +103,15 @@ hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t 
 hipError_t launch_backward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
                          int npix3, float* grads, float* losses, hipStream_t s);
+// 256 floats passed by value to the sRGB kernels: the byte thresholds of the
+// encoding (entry k the smallest linear value whose byte is k; entry 0 unused)
+// or the decoded value of each byte.
+struct SrgbTable {
+    float v[256];
+};
+hipError_t launch_encode_srgb(const float* in, int64_t n, uint8_t* out, const SrgbTable& thresholds, hipStream_t s);
+hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const SrgbTable& values, hipStream_t s);
+
 hipError_t launch_adam(float* params, const float* grads, float* m, float* v, const float* lr, int n,
                        float beta1, float beta2, float eps, float bc1, float bc2, int project,
                        hipStream_t s);

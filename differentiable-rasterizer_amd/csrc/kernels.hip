@@ -1093,6 +1093,57 @@ __global__ __launch_bounds__(256) void fit_tail(int iter, const float* __restric
     }
 }
 
+// ---------------------------------------------------------------- sRGB bytes
+
+// canvas.rs:100-105 encode_srgb, one value per thread: the byte is the number
+// of thresholds t_1 < ... < t_255 at or below v (t_k the smallest linear value
+// the reference encodes to k), found by an 8-step binary search in LDS. The
+// reference's encoding is monotonic in v on [0, 1] (checked over every float
+// there) and constant outside it after its clamp, so the count is its byte;
+// NaN compares false everywhere and gives 0, as its saturating cast does.
+__global__ __launch_bounds__(256) void encode_srgb_kernel(const float* __restrict__ in, int64_t n,
+                                                          uint8_t* __restrict__ out, SrgbTable thr) {
+    __shared__ float t[256];
+    t[threadIdx.x] = thr.v[threadIdx.x];
+    __syncthreads();
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float v = in[i];
+        int b = 0;
+#pragma unroll
+        for (int step = 128; step >= 1; step >>= 1) b += (t[b + step] <= v) ? step : 0;
+        out[i] = (uint8_t)b;
+    }
+}
+
+// canvas.rs:108-115 decode_srgb: a lookup in the table of all 256 values.
+__global__ __launch_bounds__(256) void decode_srgb_kernel(const uint8_t* __restrict__ in, int64_t n,
+                                                          float* __restrict__ out, SrgbTable val) {
+    __shared__ float t[256];
+    t[threadIdx.x] = val.v[threadIdx.x];
+    __syncthreads();
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = t[in[i]];
+}
+
+static dim3 stream_grid(int64_t n) {
+    // enough blocks to fill the chip a few times over; the loops stride the rest
+    const int64_t blocks = (n + 255) / 256;
+    return dim3((unsigned)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192));
+}
+
+hipError_t launch_encode_srgb(const float* in, int64_t n, uint8_t* out, const SrgbTable& thresholds, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(encode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, thresholds);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const SrgbTable& values, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(decode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, values);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launchers
 
 hipError_t launch_fit_tail(int iter, const float* loss, float* params, const float* grads, float* m, float* v,

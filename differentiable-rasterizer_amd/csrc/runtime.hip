@@ -56,6 +56,8 @@ enum Kind : uint64_t {
     K_PIXSTATE,
     K_TILE_ENT,
     K_TILE_N,
+    K_SRGB_F32,
+    K_SRGB_U8,
 };
 
 // Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
@@ -428,6 +430,66 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
 
 }  // namespace
 
+// ---------------------------------------------------------------- sRGB bytes
+
+namespace {
+
+// canvas.rs:100-105, with the reference's f32 operations in its order (no
+// contraction: the library is built with -ffp-contract=off) and the host
+// libm's powf, which is what Rust's f32::powf calls on Linux.
+uint8_t encode_srgb_host(float v) {
+    if (v < 0.0f) v = 0.0f;  // f32::clamp: NaN passes through
+    if (v > 1.0f) v = 1.0f;
+    const float s = v <= 0.0031308f ? 12.92f * v : 1.055f * std::pow(v, 1.0f / 2.4f) - 0.055f;
+    const float b = s * 255.0f + 0.5f;
+    if (!(b >= 0.0f)) return 0;  // `as u8` saturates, NaN -> 0
+    if (b >= 255.0f) return 255;
+    return (uint8_t)b;
+}
+
+// canvas.rs:108-115
+float decode_srgb_host(uint8_t byte) {
+    const float v = (float)byte / 255.0f;
+    if (v <= 0.04045f) return v / 12.92f;
+    return std::pow((v + 0.055f) / 1.055f, 2.4f);
+}
+
+float float_of_bits(uint32_t b) {
+    float f;
+    std::memcpy(&f, &b, sizeof f);
+    return f;
+}
+
+struct SrgbTables {
+    drh::SrgbTable thresholds, values;
+};
+
+// Entry k of the thresholds: the smallest float in [0, 1] that encodes to k or
+// more, by bisection over the bit patterns (ordered like the values there);
+// the encoding is monotonic on [0, 1].
+const SrgbTables& srgb_tables() {
+    static SrgbTables t;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        t.thresholds.v[0] = 0.0f;
+        for (int k = 1; k < 256; k++) {
+            uint32_t lo = 0, hi = 0x3F800000u;  // encode(0) = 0 < k <= encode(1) = 255
+            while (lo + 1 < hi) {
+                const uint32_t mid = lo + (hi - lo) / 2;
+                if (encode_srgb_host(float_of_bits(mid)) >= k)
+                    hi = mid;
+                else
+                    lo = mid;
+            }
+            t.thresholds.v[k] = float_of_bits(hi);
+        }
+        for (int b = 0; b < 256; b++) t.values.v[b] = decode_srgb_host((uint8_t)b);
+    });
+    return t;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* drh_last_error(void) { return g_err.c_str(); }
@@ -641,6 +703,54 @@ int drh_adam_project_step(drh_ctx* ctx, float* params, const float* grads, float
         HIP_TRY(hipMemcpyAsync(m, dm, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
         HIP_TRY(hipMemcpyAsync(v, dv, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
     }
+    return finish(flags, s);
+}
+
+int drh_encode_srgb(drh_ctx* ctx, const float* values, int64_t n, uint8_t* out, void* stream, uint32_t flags) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (n < 0) return fail(DRH_ERR_INVALID_ARG, "negative count");
+    if (n == 0) return DRH_OK;
+    if (!values || !out) return fail(DRH_ERR_INVALID_ARG, "NULL array");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const bool host = flags & DRH_HOST_PTRS;
+    Staged in;
+    int rc;
+    if ((rc = stage_in(ctx, in, K_SRGB_F32, values, (size_t)n, host, s))) return rc;
+    Lease ob;
+    uint8_t* dout = out;
+    if (host) {
+        if ((rc = ob.acquire(ctx, K_SRGB_U8, (size_t)n, s))) return rc;
+        dout = ob.get<uint8_t>();
+    }
+    HIP_TRY(drh::launch_encode_srgb(in.dev, n, dout, srgb_tables().thresholds, s), "encode_srgb launch");
+    if (host) {
+        hipError_t e = hipMemcpyAsync(out, dout, (size_t)n, hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) return fail(DRH_ERR_READBACK, std::string("hipMemcpyAsync D2H: ") + hipGetErrorString(e));
+    }
+    return finish(flags, s);
+}
+
+int drh_decode_srgb(drh_ctx* ctx, const uint8_t* bytes, int64_t n, float* out, void* stream, uint32_t flags) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (n < 0) return fail(DRH_ERR_INVALID_ARG, "negative count");
+    if (n == 0) return DRH_OK;
+    if (!bytes || !out) return fail(DRH_ERR_INVALID_ARG, "NULL array");
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const bool host = flags & DRH_HOST_PTRS;
+    Lease ib;
+    const uint8_t* din = bytes;
+    int rc;
+    if (host) {
+        if ((rc = ib.acquire(ctx, K_SRGB_U8, (size_t)n, s))) return rc;
+        HIP_TRY(hipMemcpyAsync(ib.get<uint8_t>(), bytes, (size_t)n, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+        din = ib.get<uint8_t>();
+    }
+    Out o;
+    if ((rc = stage_out(ctx, o, K_SRGB_F32, out, (size_t)n, host, s))) return rc;
+    HIP_TRY(drh::launch_decode_srgb(din, n, o.dev, srgb_tables().values, s), "decode_srgb launch");
+    if ((rc = copy_back(o, s))) return rc;
     return finish(flags, s);
 }
 

@@ -107,6 +107,8 @@ SIGNATURES = {
     "drh_fit_validate": ([ctypes.POINTER(FitConfig), _I64], ctypes.c_int),
     "drh_fit": ([_P, _P, _I64, _I64, _P, _P, _I64, ctypes.POINTER(FitConfig), _P, _P, _P,
                  ctypes.POINTER(FitReport), _P, _U32], ctypes.c_int),
+    "drh_encode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
+    "drh_decode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
 }
 
 _lib = None
@@ -231,7 +233,27 @@ class Context:
         check(lib().drh_backward_from_grad(self.handle, params, bgs, grad_images, B, T, H, W, sigma,
                                            grads, stream, flags))
 
+    def encode_srgb_ptr(self, values, n, out, stream=None, flags=0):
+        check(lib().drh_encode_srgb(self.handle, values, n, out, stream, flags))
+
+    def decode_srgb_ptr(self, data, n, out, stream=None, flags=0):
+        check(lib().drh_decode_srgb(self.handle, data, n, out, stream, flags))
+
     # -- host (numpy) forms, synchronous --------------------------------------
+    def encode_srgb(self, values) -> np.ndarray:
+        """canvas.rs:100-105 per value: linear float32 to sRGB bytes, same shape."""
+        v = _f32(values)
+        out = np.empty(v.shape, np.uint8)
+        self.encode_srgb_ptr(_ptr(v), v.size, out.ctypes.data_as(ctypes.c_void_p), flags=HOST_PTRS)
+        return out
+
+    def decode_srgb(self, data) -> np.ndarray:
+        """canvas.rs:108-115 per byte: sRGB bytes to linear float32, same shape."""
+        b = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.empty(b.shape, np.float32)
+        self.decode_srgb_ptr(b.ctypes.data_as(ctypes.c_void_p), b.size, _ptr(out), flags=HOST_PTRS)
+        return out
+
     def render(self, params, height: int, width: int, sigma: float, background=(0, 0, 0),
                exact: bool = False) -> np.ndarray:
         p = _f32(params)

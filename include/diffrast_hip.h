@@ -173,6 +173,17 @@ int drh_fit(drh_ctx *ctx, const float *target, int64_t H, int64_t W, const float
             float *out_best_params, float *out_params, drh_fit_report *report, void *stream,
             uint32_t flags);
 
+/* The gamma of Canvas::save_png (crates/diffrast/src/canvas.rs:61-68):
+ * encode_srgb (canvas.rs:100-105) of n linear values, in any layout, to sRGB
+ * bytes; clamped to [0, 1], NaN to 0. Bit-identical to the reference. */
+int drh_encode_srgb(drh_ctx *ctx, const float *values, int64_t n, uint8_t *out, void *stream,
+                    uint32_t flags);
+
+/* The gamma of Canvas::load_image (canvas.rs:70-86): decode_srgb
+ * (canvas.rs:108-115) of n sRGB bytes to linear values. */
+int drh_decode_srgb(drh_ctx *ctx, const uint8_t *bytes, int64_t n, float *out, void *stream,
+                    uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -692,3 +692,53 @@ int orc_pixel_bounds(const float *tri, size_t W, size_t H, float sigma, uint64_t
     out[3] = y1;
     return 1;
 }
+
+/* ---------------------------------------------------------------- sRGB */
+
+/* Rust `f32 as u8`: saturating, NaN -> 0. */
+static inline uint8_t sat_u8(float v) {
+    if (!(v >= 0.0f)) return 0;
+    if (v >= 255.0f) return 255;
+    return (uint8_t)v;
+}
+
+/* canvas.rs:100-105 */
+uint8_t orc_encode_srgb1(float v) {
+    v = rclamp(v, 0.0f, 1.0f);
+    float s = v <= 0.0031308f ? 12.92f * v : 1.055f * powf(v, 1.0f / 2.4f) - 0.055f;
+    return sat_u8(s * 255.0f + 0.5f);
+}
+
+/* canvas.rs:108-115 */
+float orc_decode_srgb1(uint8_t b) {
+    float v = (float)b / 255.0f;
+    if (v <= 0.04045f) return v / 12.92f;
+    return powf((v + 0.055f) / 1.055f, 2.4f);
+}
+
+void orc_encode_srgb(const float *v, size_t n, uint8_t *out) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_encode_srgb1(v[i]);
+}
+
+void orc_decode_srgb(const uint8_t *v, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_decode_srgb1(v[i]);
+}
+
+uint64_t orc_srgb_encode_scan(float thresholds[256]) {
+    uint64_t drops = 0;
+    int prev = 0;
+    for (int k = 0; k < 256; k++) thresholds[k] = k == 0 ? 0.0f : INFINITY;
+    /* Below 2^-14 the linear branch gives 12.92 v 255 + 0.5 < 0.71: byte 0,
+     * monotonic by construction (each step is a monotone rounding). From there,
+     * every float up to 1.0f in increasing order of value. */
+    if (orc_encode_srgb1(0x1p-14f) != 0) return UINT64_MAX;
+    for (uint32_t bits = 0x38800000u; bits <= 0x3F800000u; bits++) {
+        float v;
+        memcpy(&v, &bits, sizeof v);
+        int b = orc_encode_srgb1(v);
+        if (b < prev) drops++;
+        for (int k = prev + 1; k <= b; k++) thresholds[k] = v;
+        if (b > prev) prev = b;
+    }
+    return drops;
+}

@@ -128,6 +128,18 @@ float orc_coverage_with_grad(const float *tri, float px, float py, float sigma,
 int orc_pixel_bounds(const float *tri, size_t W, size_t H, float sigma,
                      uint64_t out[4]);
 
+/* canvas.rs:100-105 encode_srgb and canvas.rs:108-115 decode_srgb, the gamma of
+ * save_png / load_image: linear f32 -> sRGB byte and back. */
+uint8_t orc_encode_srgb1(float v);
+float orc_decode_srgb1(uint8_t v);
+void orc_encode_srgb(const float *v, size_t n, uint8_t *out);
+void orc_decode_srgb(const uint8_t *v, size_t n, float *out);
+/* Over every f32 in [2^-14, 1] (below it every byte is 0), the number of inputs
+ * whose byte is below the byte of the next smaller float (0 when encode_srgb is
+ * monotonic there), and the smallest input giving each byte 1..255
+ * (thresholds[0] = 0). */
+uint64_t orc_srgb_encode_scan(float thresholds[256]);
+
 #ifdef __cplusplus
 }
 #endif

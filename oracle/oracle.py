@@ -97,6 +97,11 @@ def lib() -> ctypes.CDLL:
         L.orc_coverage_with_grad.restype = ctypes.c_float
         L.orc_pixel_bounds.argtypes = [_F, _SZ, _SZ, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]
         L.orc_pixel_bounds.restype = ctypes.c_int
+        _U8 = ctypes.POINTER(ctypes.c_uint8)
+        L.orc_encode_srgb.argtypes = [_F, _SZ, _U8]
+        L.orc_decode_srgb.argtypes = [_U8, _SZ, _F]
+        L.orc_srgb_encode_scan.argtypes = [_F]
+        L.orc_srgb_encode_scan.restype = ctypes.c_uint64
         _lib = L
     return _lib
 
@@ -317,3 +322,26 @@ def pixel_bounds(tri, width: int, height: int, sigma: float):
 
 def cpu_count() -> int:
     return os.cpu_count() or 1
+
+
+def encode_srgb(values) -> np.ndarray:
+    """canvas.rs:100-105 per value."""
+    v = _f32(values)
+    out = np.empty(v.shape, np.uint8)
+    lib().orc_encode_srgb(_p(v), v.size, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+    return out
+
+
+def decode_srgb(data) -> np.ndarray:
+    """canvas.rs:108-115 per byte."""
+    b = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(b.shape, np.float32)
+    lib().orc_decode_srgb(b.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), b.size, _p(out))
+    return out
+
+
+def srgb_encode_scan():
+    """(count of monotonicity breaks of encode_srgb over [2^-14, 1], thresholds[256])."""
+    thr = np.zeros(256, np.float32)
+    drops = lib().orc_srgb_encode_scan(_p(thr))
+    return int(drops), thr
