@@ -42,9 +42,11 @@ enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4, F_CCW = 8 };
 enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2 };
 
 // Contributing entries the forward kernel records per tile for the backward
-// kernel (over all chunks); beyond it the backward kernel rebuilds and
-// reclassifies the remaining chunks.
-constexpr int CAP2 = 128;
+// kernel (over all chunks) are RasterArgs::cap2, at least CAP2_MIN. When cap2
+// covers T every tile's list is recorded whole and the backward kernel is the
+// variant without the rebuild path; otherwise a tile past cap2 rebuilds and
+// reclassifies its remaining chunks there.
+constexpr int CAP2_MIN = 128;
 
 // One recorded entry of a tile's list, written by the forward kernel and read
 // (with scalar loads) by the backward kernel.
@@ -74,7 +76,8 @@ struct RasterArgs {
     float* partials;       // B*nblk*T*NP
     double* partial_loss;  // B*nblk
     PixState* pstate;      // B*H*W
-    TileEnt* tl_ent;       // ntiles*CAP2 recorded entries
+    TileEnt* tl_ent;       // ntiles*cap2 recorded entries
+    int cap2;              // entries recorded per tile
     int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)
@@ -100,7 +103,7 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
                         float* rec, float* zero_grads, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
-hipError_t launch_backward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
+hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s);
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
                          int npix3, float* grads, float* losses, hipStream_t s);
 // 256 floats passed by value to the sRGB kernels: the byte thresholds of the

@@ -681,9 +681,10 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     Trans tot = {1.0f, 0, 0};
 
     const int n_chunks = (T + CH - 1) / CH;
-    int n2 = 0;                 // contributing entries seen (recorded while n2 < CAP2)
+    int n2 = 0;                 // contributing entries seen (recorded while n2 < cap2)
     int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
-    TileEnt* te = a.tl_ent + tg.tile * CAP2;
+    const int cap2 = a.cap2;
+    TileEnt* te = a.tl_ent + tg.tile * cap2;
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -714,7 +715,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                 uint64_t onm = __ballot(on);
                 if (onm != 0) {
                     const uint64_t bm = __ballot(on && band);
-                    if (n2 < CAP2 && lane == 0) {
+                    if (n2 < cap2 && lane == 0) {
                         TileEnt e;
                         e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
                         e.pad = 0;
@@ -726,7 +727,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                 }
             }
         }
-        if (n2 > CAP2 && rec_chunks == n_chunks) rec_chunks = c;
+        if (n2 > cap2 && rec_chunks == n_chunks) rec_chunks = c;
     }
 
     if (MODE == MODE_RENDER || (MODE == MODE_LOSS && a.out_img)) {
@@ -739,7 +740,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     if (MODE == MODE_RENDER) return;
 
     if (lane == 0) {
-        a.tl_n[2 * tg.tile] = min(n2, CAP2);
+        a.tl_n[2 * tg.tile] = min(n2, cap2);
         a.tl_n[2 * tg.tile + 1] = rec_chunks;
     }
     PixState ps;
@@ -847,8 +848,11 @@ __device__ inline void reduce_entry(const float (&a)[NP], bool any_band, float* 
 // of transmittance products instead of being peeled off a tape. Per-triangle
 // gradients are wave-reduced, accumulated per wave in LDS and written as one
 // partial row per block and chunk.
-template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(6))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
+// REBUILD: with the rebuild path for tiles past the recorded entries. Without
+// it (the entries cover T, the usual case) the kernel needs ~55 VGPRs instead
+// of ~95, so it runs uncapped.
+template <int MODE, bool FAST, bool REBUILD>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? 6 : 7))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
                                                                const TileEnt* __restrict__ ents) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ float acc[WAVES][CH * NP];
@@ -876,7 +880,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(6)))
     const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
     const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
     // wave-uniform, so the recorded entries are read with scalar loads
-    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * CAP2;
+    const int cap2 = a.cap2;
+    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
     const size_t blk = tg.tile / WAVES;
     float* accw = acc[wave];
     const int p10 = red10_param(lane);
@@ -894,12 +899,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(6)))
             // The entries the forward kernel recorded: which lanes contribute
             // and which of them took the exact path are known; only w is
             // recomputed. The next entry is read one iteration ahead.
-            TileEnt nx = te[min(i2, CAP2 - 1)];
+            TileEnt nx = te[min(i2, cap2 - 1)];
             for (; i2 < n2r; i2++) {
                 const TileEnt cur = nx;
                 const int k = (int)(cur.k >> 8);
                 if (k >= k1) break;
-                nx = te[min(i2 + 1, CAP2 - 1)];
+                nx = te[min(i2 + 1, cap2 - 1)];
                 const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
                 const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
                 const float* rp = rec + (size_t)k * REC;
@@ -912,7 +917,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(6)))
                 grad_pixel(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
                 reduce_entry(part, cur.band != 0, accw + (k - k0) * NP, lane, p10);
             }
-        } else {
+        } else if (REBUILD) {
             // Fallback when the forward kernel ran out of record space: rebuild
             // the chunk's list and classify every pair again.
             int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
@@ -1174,10 +1179,10 @@ static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int MODE, bool FAST>
+template <int MODE, bool FAST, bool REBUILD>
 static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((backward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec,
-                       a.tl_ent);
+    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s,
+                       a, a.rec, a.tl_ent);
     return hipGetLastError();
 }
 
@@ -1189,10 +1194,15 @@ hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t 
     return fast ? launch_forward_t<MODE_GRAD_IN, true>(a, s) : launch_forward_t<MODE_GRAD_IN, false>(a, s);
 }
 
-hipError_t launch_backward(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
+hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s) {
+    if (rebuild) {
+        if (mode == MODE_LOSS)
+            return fast ? launch_backward_t<MODE_LOSS, true, true>(a, s) : launch_backward_t<MODE_LOSS, false, true>(a, s);
+        return fast ? launch_backward_t<MODE_GRAD_IN, true, true>(a, s) : launch_backward_t<MODE_GRAD_IN, false, true>(a, s);
+    }
     if (mode == MODE_LOSS)
-        return fast ? launch_backward_t<MODE_LOSS, true>(a, s) : launch_backward_t<MODE_LOSS, false>(a, s);
-    return fast ? launch_backward_t<MODE_GRAD_IN, true>(a, s) : launch_backward_t<MODE_GRAD_IN, false>(a, s);
+        return fast ? launch_backward_t<MODE_LOSS, true, false>(a, s) : launch_backward_t<MODE_LOSS, false, false>(a, s);
+    return fast ? launch_backward_t<MODE_GRAD_IN, true, false>(a, s) : launch_backward_t<MODE_GRAD_IN, false, false>(a, s);
 }
 
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,

@@ -7,6 +7,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -364,6 +365,23 @@ class KernelTimer {
     bool on_ = false;
 };
 
+// Entries the forward kernel records per tile: all T (the backward kernel then
+// needs no rebuild path) while that fits TILE_ENT_BUDGET bytes, else as many as
+// fit, at least CAP2_MIN. DRH_MAX_TILE_ENTRIES (environment) lowers the cap, so
+// tests can force the rebuild path.
+constexpr size_t TILE_ENT_BUDGET = 1ull << 30;
+
+int tile_entries(size_t ntiles, int T) {
+    size_t cap = (size_t)(T > 0 ? T : 1);
+    const size_t fit = TILE_ENT_BUDGET / (ntiles * sizeof(drh::TileEnt));
+    if (cap > fit) cap = fit > (size_t)drh::CAP2_MIN ? fit : (size_t)drh::CAP2_MIN;
+    if (const char* e = std::getenv("DRH_MAX_TILE_ENTRIES")) {
+        const long v = std::strtol(e, nullptr, 10);
+        if (v >= 1 && (size_t)v < cap) cap = (size_t)v;
+    }
+    return (int)cap;
+}
+
 // The shared raster sequence: records, the forward pass, and (for the
 // gradient modes) the backward pass and the partial-row reduction.
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
@@ -375,6 +393,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     int nblk = (int)(grid.x * grid.y);
     size_t ntiles = (size_t)B * nblk * drh::WAVES;
     Lease rec, partials, ploss, pstate, tent, tn;
+    const int cap2 = tile_entries(ntiles, T);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
     if (mode != drh::MODE_RENDER) {
@@ -382,7 +401,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
             return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
         if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
-        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * drh::CAP2 * sizeof(drh::TileEnt), s))) return rc;
+        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * cap2 * sizeof(drh::TileEnt), s))) return rc;
         if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
     }
     {
@@ -406,6 +425,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.partial_loss = ploss.get<double>();
     a.pstate = pstate.get<drh::PixState>();
     a.tl_ent = tent.get<drh::TileEnt>();
+    a.cap2 = cap2;
     a.tl_n = tn.get<int>();
     a.grads = out_grads;
     a.losses = out_losses;
@@ -417,7 +437,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     if (mode != drh::MODE_RENDER) {
         {
             KernelTimer kt(ctx, TK_BACKWARD, s);
-            HIP_TRY(drh::launch_backward(mode, fast, a, s), "backward_kernel launch");
+            HIP_TRY(drh::launch_backward(mode, fast, cap2 < T, a, s), "backward_kernel launch");
         }
         if (!det) return DRH_OK;
         KernelTimer kt(ctx, TK_REDUCE, s);

@@ -306,3 +306,22 @@ def test_device_fit_stop_reasons(ctx):
     bad[3, 4, 1] = float("nan")
     r = ctx.fit(bad, init, bg, iters=10)  # fit.rs:259-265
     assert r["stop_reason"] == "Diverged" and len(r["losses"]) == 0
+
+
+def test_rebuild_path_past_the_recorded_entries(ctx, orc, monkeypatch):
+    # Tiles keep at most DRH_MAX_TILE_ENTRIES recorded entries; past them the
+    # backward kernel rebuilds and reclassifies the remaining chunks.
+    params, bgs = make_case(2, 40, 48, 300, "small")
+    targets = synth.batch("small", 2, 300, 900)
+    targets = orc.render_batch(targets, 40, 48, 0.004, bgs)
+    want_l, want_g = orc.loss_backward_batch(params, targets, 0.004, bgs)
+    for cap in ("3", "40", "1"):
+        monkeypatch.setenv("DRH_MAX_TILE_ENTRIES", cap)
+        print(f"rebuild cap={cap}", flush=True)
+        for det in (False, True):
+            l, g = ctx.fused_loss_backward(params, targets, 0.004, bgs, deterministic=det)
+            check_losses(l, want_l)
+            assert grad_err(g, want_g) <= GRAD_RTOL
+        gi = np.random.default_rng(1).standard_normal((2, 40, 48, 3)).astype(np.float32) * 1e-3
+        g2 = ctx.backward_from_grad(params, gi, 0.004, bgs)
+        assert grad_err(g2, orc.backward_from_grad_batch(params, gi, 0.004, bgs)) <= GRAD_RTOL
