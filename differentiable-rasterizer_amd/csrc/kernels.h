@@ -82,6 +82,7 @@ struct RasterArgs {
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)
     int deterministic;     // per-block partial rows + reduce_partials instead of atomics
+    int chw;               // images, targets and grad_in are B x 3 x H x W (else B x H x W x 3)
 };
 
 // Device-side state of a running fit (fit.rs:197-211).

@@ -618,6 +618,13 @@ __device__ inline float trans_suffix(const Trans& total, const Trans& prefix) {
     return total.z != prefix.z ? 0.0f : ratio;
 }
 
+// Index of channel ch of this lane's pixel in an image array: B x H x W x 3, or
+// B x 3 x H x W when a.chw.
+__device__ inline size_t img_index(const RasterArgs& a, size_t pix, int b, int ch) {
+    const size_t hw = (size_t)a.H * a.W;
+    return a.chw ? ((size_t)b * 3 + ch) * hw + (pix - (size_t)b * hw) : pix * 3 + ch;
+}
+
 // Tile geometry shared by both kernels: one wave per 8x8 tile, four tiles
 // (2x2) per block, one pixel per lane.
 struct TileGeo {
@@ -732,9 +739,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
 
     if (MODE == MODE_RENDER || (MODE == MODE_LOSS && a.out_img)) {
         if (tg.valid) {
-            a.out_img[tg.pix * 3 + 0] = col[0];
-            a.out_img[tg.pix * 3 + 1] = col[1];
-            a.out_img[tg.pix * 3 + 2] = col[2];
+            a.out_img[img_index(a, tg.pix, b, 0)] = col[0];
+            a.out_img[img_index(a, tg.pix, b, 1)] = col[1];
+            a.out_img[img_index(a, tg.pix, b, 2)] = col[2];
         }
     }
     if (MODE == MODE_RENDER) return;
@@ -753,7 +760,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
         if (tg.valid) {
             float scale = 2.0f / (float)(3 * (size_t)W * H);
             for (int ch = 0; ch < 3; ch++) {
-                float t = a.target[tg.pix * 3 + ch];
+                float t = a.target[img_index(a, tg.pix, b, ch)];
                 float d = col[ch] - t;
                 l += (double)d * (double)d;
                 ps.g0[ch] = scale * (col[ch] - t);
@@ -868,7 +875,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
         PixState ps = a.pstate[tg.pix];
         st.tot = {ps.q, ps.z, ps.e};
         for (int ch = 0; ch < 3; ch++) {
-            st.g0[ch] = !tg.valid ? 0.0f : (MODE == MODE_LOSS ? ps.g0[ch] : a.grad_in[tg.pix * 3 + ch]);
+            st.g0[ch] = !tg.valid ? 0.0f
+                                  : (MODE == MODE_LOSS ? ps.g0[ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
         }
     }
     st.col[0] = a.bg[b * 3 + 0];

@@ -430,6 +430,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.grads = out_grads;
     a.losses = out_losses;
     a.deterministic = det ? 1 : 0;
+    a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
     {
         KernelTimer kt(ctx, TK_RASTER, s);
         HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
@@ -849,7 +850,7 @@ int drh_fit(drh_ctx* ctx, const float* target, int64_t H, int64_t W, const float
         // Fixed-order gradient sums: a fit with a given start is reproducible,
         // as the reference's is (fit.rs:487-496).
         if ((rc = run_raster(ctx, drh::MODE_LOSS, d_params, bg.dev, tg.dev, 1, (int)T, (int)H, (int)W, sigma,
-                             nullptr, d_grads, d_loss, flags | DRH_DETERMINISTIC, s)))
+                             nullptr, d_grads, d_loss, (flags & ~DRH_CHANNELS_FIRST) | DRH_DETERMINISTIC, s)))
             return rc;
         int32_t t = (int32_t)(i + 1);
         float bc1 = 1.0f - powi_f32(beta1, t), bc2 = 1.0f - powi_f32(beta2, t);

@@ -29,6 +29,7 @@ HOST_PTRS = 0x1
 SYNC = 0x2
 EXACT_MATH = 0x4
 DETERMINISTIC = 0x8
+CHANNELS_FIRST = 0x10
 
 STOP_REASONS = {0: "Completed", 1: "Converged", 2: "Diverged"}
 CONFIG_ERRORS = {1: "NoTriangles", 2: "NonPositiveSigma", 3: "SigmaNotDecreasing",

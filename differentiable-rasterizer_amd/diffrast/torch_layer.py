@@ -80,11 +80,31 @@ def _on_gpu(t: Tensor, dev: torch.device) -> Tensor:
     return t.detach().to(device=dev, dtype=torch.float32).contiguous()
 
 
+_bg_cache: dict = {}
+
+
 def _backgrounds(background, B: int, dev: torch.device) -> Tensor:
-    bg = torch.as_tensor(background, dtype=torch.float32)
-    if bg.numel() != 3:
+    """The (B, 3) device array of one background colour, cached: a host-to-device
+    copy of pageable memory per call would wait for the stream's queued work."""
+    if isinstance(background, Tensor):
+        bg = background.detach().to(dtype=torch.float32)
+        if bg.numel() != 3:
+            raise ValueError("background must have 3 components")
+        return bg.reshape(1, 3).expand(B, 3).to(dev).contiguous()
+    vals = tuple(float(v) for v in background)
+    if len(vals) != 3:
         raise ValueError("background must have 3 components")
-    return bg.reshape(1, 3).expand(B, 3).contiguous().to(dev)
+    key = (dev.index, B, vals)
+    with _ctx_lock:
+        bg = _bg_cache.get(key)
+    if bg is None:
+        bg = torch.tensor(vals, dtype=torch.float32).reshape(1, 3).expand(B, 3).contiguous().to(dev)
+        torch.cuda.current_stream(dev).synchronize()  # usable from any stream from now on
+        with _ctx_lock:
+            if len(_bg_cache) >= 64:
+                _bg_cache.clear()
+            _bg_cache[key] = bg
+    return bg
 
 
 def _note_gpu() -> None:
@@ -92,14 +112,16 @@ def _note_gpu() -> None:
     _last_device = "gpu"
 
 
-def _render(params: Tensor, height: int, width: int, sigma: float, background) -> Tensor:
+def _render(params: Tensor, height: int, width: int, sigma: float, background, channels_first: bool) -> Tensor:
+    """(B, 3, H, W) or (B, H, W, 3), written in that layout by the kernel."""
     dev = _gpu()
     p = _on_gpu(params, dev)
     B, T = p.shape[0], p.shape[1]
     bg = _backgrounds(background, B, dev)
-    out = torch.empty((B, height, width, 3), device=dev, dtype=torch.float32)
+    shape = (B, 3, height, width) if channels_first else (B, height, width, 3)
+    out = torch.empty(shape, device=dev, dtype=torch.float32)
     _context(dev).render_ptr(p.data_ptr(), bg.data_ptr(), B, T, height, width, float(sigma),
-                             out.data_ptr(), _stream(dev))
+                             out.data_ptr(), _stream(dev), _lib.CHANNELS_FIRST if channels_first else 0)
     _note_gpu()
     return out
 
@@ -108,12 +130,14 @@ class _Rasterize(torch.autograd.Function):
     """Forward renders, backward maps dL/dimage to dL/dparams (torch_layer.py:37-66)."""
 
     @staticmethod
-    def forward(ctx, params: Tensor, height: int, width: int, sigma: float, background, device):
-        images = _render(params, height, width, sigma, background)
+    def forward(ctx, params: Tensor, height: int, width: int, sigma: float, background, device,
+                channels_first: bool):
+        images = _render(params, height, width, sigma, background, channels_first)
         ctx.save_for_backward(params)
         ctx.sigma = sigma
         ctx.background = background
         ctx.device = device
+        ctx.channels_first = channels_first
         return images
 
     @staticmethod
@@ -123,13 +147,14 @@ class _Rasterize(torch.autograd.Function):
         p = _on_gpu(params, dev)
         g = _on_gpu(grad_images, dev)
         B, T = p.shape[0], p.shape[1]
-        H, W = g.shape[1], g.shape[2]
+        H, W = (g.shape[2], g.shape[3]) if ctx.channels_first else (g.shape[1], g.shape[2])
         bg = _backgrounds(ctx.background, B, dev)
         grads = torch.empty((B, T, N_PARAMS), device=dev, dtype=torch.float32)
         _context(dev).from_grad_ptr(p.data_ptr(), bg.data_ptr(), g.data_ptr(), B, T, H, W,
-                                    float(ctx.sigma), grads.data_ptr(), _stream(dev))
+                                    float(ctx.sigma), grads.data_ptr(), _stream(dev),
+                                    _lib.CHANNELS_FIRST if ctx.channels_first else 0)
         _note_gpu()
-        return grads.to(params.device, params.dtype), None, None, None, None, None
+        return grads.to(params.device, params.dtype), None, None, None, None, None, None
 
 
 def rasterize(
@@ -164,29 +189,30 @@ def rasterize(
     _check_sigma(sigma)
     _parse_device(device)
 
-    images = _Rasterize.apply(params, height, width, sigma, background, device)
-    images = images.to(params.device, params.dtype)
-    return images.permute(0, 3, 1, 2).contiguous() if channels_first else images
+    images = _Rasterize.apply(params, height, width, sigma, background, device, bool(channels_first))
+    return images.to(params.device, params.dtype)
 
 
-def _fused(params: Tensor, targets_hwc: Tensor, sigma: float, background):
-    """(losses (B,), grads (B, T, 10)) on the GPU, float32."""
+def _fused(params: Tensor, targets: Tensor, sigma: float, background, channels_first: bool = False):
+    """(losses (B,), grads (B, T, 10)) on the GPU, float32; targets (B, H, W, 3), or
+    (B, 3, H, W) when channels_first (read in place, no transposing copy)."""
     dev = _gpu()
     p = _on_gpu(params, dev)
-    t = _on_gpu(targets_hwc, dev)
+    t = _on_gpu(targets, dev)
     B, T = p.shape[0], p.shape[1]
     if t.shape[0] != B:
         raise ValueError(f"batch mismatch: {B} parameter rows but {t.shape[0]} targets")
-    if t.shape[3] != 3:
+    if t.shape[1 if channels_first else 3] != 3:
         raise ValueError("targets must have 3 channels")
-    H, W = t.shape[1], t.shape[2]
+    H, W = (t.shape[2], t.shape[3]) if channels_first else (t.shape[1], t.shape[2])
     if H == 0 or W == 0:
         raise ValueError("height and width must be non-zero")
     bg = _backgrounds(background, B, dev)
     losses = torch.empty((B,), device=dev, dtype=torch.float32)
     grads = torch.empty((B, T, N_PARAMS), device=dev, dtype=torch.float32)
     _context(dev).fused_ptr(p.data_ptr(), bg.data_ptr(), t.data_ptr(), B, T, H, W, float(sigma),
-                            losses.data_ptr(), grads.data_ptr(), None, _stream(dev))
+                            losses.data_ptr(), grads.data_ptr(), None, _stream(dev),
+                            _lib.CHANNELS_FIRST if channels_first else 0)
     _note_gpu()
     return losses, grads
 
@@ -196,7 +222,7 @@ class _FusedMSE(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, params: Tensor, targets: Tensor, sigma: float, background, device):
-        losses, grads = _fused(params, targets, sigma, background)
+        losses, grads = _fused(params, targets, sigma, background, channels_first=True)
         ctx.save_for_backward(grads.to(params.device, params.dtype))
         ctx.batch = len(params)
         return losses.mean().to(params.device, params.dtype)
@@ -232,8 +258,7 @@ def fused_mse(
     _check_sigma(sigma)
     _parse_device(device)
 
-    hwc = targets.permute(0, 2, 3, 1).contiguous()
-    return _FusedMSE.apply(params, hwc, sigma, background, device)
+    return _FusedMSE.apply(params, targets, sigma, background, device)
 
 
 def gpu_adapter() -> str | None:
@@ -258,6 +283,7 @@ def shutdown_gpu() -> bool:
         for ctx in _contexts.values():
             ctx.close()
         _contexts.clear()
+        _bg_cache.clear()
     return released
 
 

@@ -50,6 +50,8 @@ enum {
 #define DRH_EXACT_MATH 0x4u /* IEEE division, sqrt and expf in the per-pixel geometry */
 #define DRH_DETERMINISTIC 0x8u /* gradients summed in a fixed order: bit-identical run to run
                                   (default: one float atomic per triangle parameter per block) */
+#define DRH_CHANNELS_FIRST 0x10u /* images, targets and grad_images are B x 3 x H x W (the
+                                    layout torch_layer.rasterize returns) instead of B x H x W x 3 */
 
 /* Bounded host wait, as GpuRasterizer::POLL_TIMEOUT (crates/diffrast-gpu/src/lib.rs:229). */
 #define DRH_WAIT_TIMEOUT_S 60

@@ -325,3 +325,37 @@ def test_rebuild_path_past_the_recorded_entries(ctx, orc, monkeypatch):
         gi = np.random.default_rng(1).standard_normal((2, 40, 48, 3)).astype(np.float32) * 1e-3
         g2 = ctx.backward_from_grad(params, gi, 0.004, bgs)
         assert grad_err(g2, orc.backward_from_grad_batch(params, gi, 0.004, bgs)) <= GRAD_RTOL
+
+
+def test_channels_first_layout_gives_the_same_numbers(ctx):
+    # DRH_CHANNELS_FIRST: images, targets and grad_images as B x 3 x H x W,
+    # the torch op's layout; every result equals the B x H x W x 3 call's.
+    import torch
+
+    from diffrast import _lib
+
+    B, H, W, T, sig = 3, 37, 29, 40, 0.004
+    params, bgs = make_case(B, H, W, T, "uniform")
+    dev = torch.device("cuda:0")
+    p, bg = torch.from_numpy(params).to(dev), torch.from_numpy(bgs).to(dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    hwc = torch.empty((B, H, W, 3), device=dev)
+    chw = torch.empty((B, 3, H, W), device=dev)
+    ctx.render_ptr(p.data_ptr(), bg.data_ptr(), B, T, H, W, sig, hwc.data_ptr(), s)
+    ctx.render_ptr(p.data_ptr(), bg.data_ptr(), B, T, H, W, sig, chw.data_ptr(), s, _lib.CHANNELS_FIRST)
+    assert torch.equal(chw, hwc.permute(0, 3, 1, 2))
+    tgt = torch.rand((B, H, W, 3), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    out = {}
+    for name, t, flags in (("hwc", tgt, 0), ("chw", tgt.permute(0, 3, 1, 2).contiguous(), _lib.CHANNELS_FIRST)):
+        l, g = torch.empty(B, device=dev), torch.empty((B, T, 10), device=dev)
+        img = torch.empty_like(t)
+        ctx.fused_ptr(p.data_ptr(), bg.data_ptr(), t.data_ptr(), B, T, H, W, sig, l.data_ptr(), g.data_ptr(),
+                      img.data_ptr(), s, flags | _lib.DETERMINISTIC)
+        gi = (t - 0.5) * 1e-3
+        g2 = torch.empty((B, T, 10), device=dev)
+        ctx.from_grad_ptr(p.data_ptr(), bg.data_ptr(), gi.data_ptr(), B, T, H, W, sig, g2.data_ptr(), s,
+                          flags | _lib.DETERMINISTIC)
+        out[name] = (l, g, img if flags == 0 else img.permute(0, 2, 3, 1), g2)
+    torch.cuda.synchronize()
+    for a, b in zip(out["hwc"], out["chw"]):
+        assert torch.equal(a, b)
