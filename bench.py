@@ -176,6 +176,30 @@ def torch_op_ms(torch, cfg, p, targets, dev, steps=10):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=10):
+    """End to end through the drop-in autograd op: rasterize, an MSE in torch, backward.
+    keep_record=False times the backward that renders again, as the reference's does."""
+    from diffrast import torch_layer
+
+    tgt = targets.permute(0, 3, 1, 2).contiguous()
+    q = p.clone().requires_grad_(True)
+
+    def step():
+        img = torch_layer._Rasterize.apply(q, cfg["H"], cfg["W"], SIGMA, (0.0, 0.0, 0.0), "gpu", True,
+                                           keep_record)
+        ((img - tgt) ** 2).mean().backward()
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        q.grad = None
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
 def forward_side(torch, ctx, dev, cpu=True):
     """Forward-only renders (drh_render): the reference's GPU forward benchmark cells, one
     Scene::random-shaped scene each at sigma 0.0015 (gpu_bench.rs:18-69), the fit binary's
@@ -364,6 +388,9 @@ def main():
                           "pixel_tri_per_s": c["B"] * c["H"] * c["W"] * c["T"] / (m / 1e3)}
         side["c4_fit_800_iters"] = fit_side(ctx)
         side["c2_torch_fused_mse_fwd_bwd_ms"] = round(torch_op_ms(torch, cfg, p, targets, dev), 4)
+        side["c2_torch_rasterize_mse_fwd_bwd_ms"] = round(torch_rasterize_ms(torch, cfg, p, targets, dev), 4)
+        side["c2_torch_rasterize_mse_fwd_bwd_rerender_ms"] = round(
+            torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=False), 4)
         side["forward_only"] = forward_side(torch, ctx, dev, cpu=not args.no_cpu_baseline)
         out["side"] = side
 

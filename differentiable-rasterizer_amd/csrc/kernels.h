@@ -37,9 +37,17 @@ enum RecField : int {
     R_EB = 52,     // 3 x 8: per edge a.x a.y e.x e.y |e|^2 1/|e|^2 0 0 (scalar-loaded by edge index)
 };
 // F_CCW: the cross products of inside points are >= 0 (else <= 0).
-enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4, F_CCW = 8 };
+// F_LIVE: drawn by this call's forward pass. F_TAPE: live for the taped forward
+// of the gradient paths, which culls a NaN alpha that a render composites; it
+// differs from F_LIVE only in records made by a render kept for a backward.
+enum : int { F_LIVE = 1, F_ACTIVE = 2, F_FAST = 4, F_CCW = 8, F_TAPE = 16 };
 
-enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2 };
+// MODE_RECORD is a forward pass only: MODE_RENDER's image plus MODE_GRAD_IN's
+// hand-over to the backward kernel, for a render whose backward comes later.
+enum : int { MODE_RENDER = 0, MODE_LOSS = 1, MODE_GRAD_IN = 2, MODE_RECORD = 3 };
+// setup_records liveness: a render's, the taped forward's, or a render's with
+// F_TAPE marking the taped forward's (MODE_RECORD).
+enum : int { SETUP_RENDER = 0, SETUP_TAPE = 1, SETUP_RECORD = 2 };
 
 // Contributing entries the forward kernel records per tile for the backward
 // kernel (over all chunks) are RasterArgs::cap2, at least CAP2_MIN. When cap2
@@ -72,7 +80,7 @@ struct RasterArgs {
     const float* bg;       // B*3
     const float* target;   // B*H*W*3 (MODE_LOSS)
     const float* grad_in;  // B*H*W*3 (MODE_GRAD_IN)
-    float* out_img;        // B*H*W*3 (MODE_RENDER; optional in MODE_LOSS)
+    float* out_img;        // B*H*W*3 (MODE_RENDER, MODE_RECORD; optional in MODE_LOSS)
     float* partials;       // B*nblk*T*NP
     double* partial_loss;  // B*nblk
     PixState* pstate;      // B*H*W
@@ -101,8 +109,12 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
                            float min_delta, long long patience, FitState* st, float* losses_out,
                            float* best_params, hipStream_t s);
 
-hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
-                        float* rec, float* zero_grads, hipStream_t s);
+// bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src.
+hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
+                        float* rec, float* zero_grads, hipStream_t s, const float* bg_src = nullptr,
+                        float* bg_dst = nullptr);
+// n floats set to zero by a kernel (no memset node, so callers may capture it).
+hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s);
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,

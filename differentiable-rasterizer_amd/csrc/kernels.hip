@@ -57,9 +57,12 @@ __device__ inline int upper_bound_px(float hi, float pad, int n) {
 }
 
 __global__ void setup_records(const float* __restrict__ params, int n_tri, int W, int H,
-                              float sigma, int tape_mode, float* __restrict__ rec,
-                              float* __restrict__ zero_grads) {
+                              float sigma, int setup_mode, float* __restrict__ rec,
+                              float* __restrict__ zero_grads, const float* __restrict__ bg_src,
+                              float* __restrict__ bg_dst, int n_bg) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
+    // A record kept for a later backward holds its own copy of the backgrounds.
+    if (bg_dst && i < n_bg) bg_dst[i] = bg_src[i];
     if (i >= n_tri) return;
     // The backward kernel adds into the gradients: they start at zero.
     if (zero_grads)
@@ -88,7 +91,8 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
     bool box_ok = finite && bx0 < bx1 && by0 < by1;
     // render (raster.rs:48-51) rejects `alpha <= 0`, which lets NaN through;
     // the taped forward (grad.rs:61-62) keeps only `alpha > 0`.
-    bool live = box_ok && (tape_mode ? (alpha > 0.0f) : !(alpha <= 0.0f));
+    const bool taped = box_ok && alpha > 0.0f;
+    bool live = setup_mode == SETUP_TAPE ? taped : box_ok && !(alpha <= 0.0f);
 
     // Edges in the reference's order: (v0,v1), (v1,v2), (v2,v0); e = b - a.
     float e[6];
@@ -136,7 +140,7 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
     ri[R_BOX + 3] = live ? by1 : 0;
     bool active = p[9] > 0.0f && p[9] < 1.0f;  // grad.rs:145
     ri[R_FLAGS] = (live ? F_LIVE : 0) | (active ? F_ACTIVE : 0) | (fast && live ? F_FAST : 0) |
-                  (area2 >= 0.0f ? F_CCW : 0);
+                  (area2 >= 0.0f ? F_CCW : 0) | (taped ? F_TAPE : 0);
     r[R_SPARE] = 0.0f;
     for (int j = 0; j < 6; j++) r[R_E + j] = e[j];
     for (int j = 0; j < 3; j++) r[R_LEN2 + j] = len2[j];
@@ -464,8 +468,8 @@ __device__ inline double wave_sum_f64(double v) {
 
 enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 
-// Builds this wave's ordered list of triangles in [k0, k1) that can touch its
-// tile. Entry: (k_local << 8) | (plan << 2) | class, with class FULL when every
+// Builds this wave's ordered list of the triangles in [k0, k1) with flag
+// `live` (F_LIVE, or F_TAPE for a backward pass) that can touch its tile. Entry: (k_local << 8) | (plan << 2) | class, with class FULL when every
 // tile pixel is inside the triangle's box and deep inside the triangle, else
 // PARTIAL, and the plan of the exact path (PLAN_* or a single edge).
 //
@@ -476,7 +480,7 @@ enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 // upper bound by more than the margin is never nearest.
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
-                                 uint32_t* list, int lane) {
+                                 uint32_t* list, int lane, int live) {
     int count = 0;
     for (int base = k0; base < k1; base += 64) {
         int k = base + lane;
@@ -486,7 +490,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
             const int* ri = reinterpret_cast<const int*>(r);
             int flags = ri[R_FLAGS];
             int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
-            if ((flags & F_LIVE) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1) {
+            if ((flags & live) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1) {
                 cls = CLS_PARTIAL;
                 const bool in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
                 if (in_box) extra |= ENT_INBOX;
@@ -696,7 +700,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
         int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0, tg.cx1,
-                                         tg.cy1, list[wave], lane)
+                                         tg.cy1, list[wave], lane, F_LIVE)
                             : 0;
         uint32_t nxt = list[wave][0];  // the next entry is read one iteration ahead
         for (int i = 0; i < count; i++) {
@@ -709,6 +713,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             bool band;
             Geo g;
             bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+            // MODE_RECORD draws what a render draws but hands over what the
+            // taped forward keeps (F_TAPE); in the other modes the two agree.
+            const bool taped = on && (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE));
             {
                 // raster.rs:60-66, kept only where the pair contributes
                 const float omw = 1.0f - w;
@@ -716,12 +723,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                     const float o = r.f(R_C + ch) * w + col[ch] * omw;
                     col[ch] = on ? o : col[ch];
                 }
-                if (MODE != MODE_RENDER) trans_mul(tot, on ? omw : 1.0f);
+                if (MODE != MODE_RENDER) trans_mul(tot, taped ? omw : 1.0f);
             }
             if (MODE != MODE_RENDER) {
-                uint64_t onm = __ballot(on);
+                uint64_t onm = __ballot(taped);
                 if (onm != 0) {
-                    const uint64_t bm = __ballot(on && band);
+                    const uint64_t bm = __ballot(taped && band);
                     if (n2 < cap2 && lane == 0) {
                         TileEnt e;
                         e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
@@ -737,7 +744,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
         if (n2 > cap2 && rec_chunks == n_chunks) rec_chunks = c;
     }
 
-    if (MODE == MODE_RENDER || (MODE == MODE_LOSS && a.out_img)) {
+    if (MODE == MODE_RENDER || MODE == MODE_RECORD || (MODE == MODE_LOSS && a.out_img)) {
         if (tg.valid) {
             a.out_img[img_index(a, tg.pix, b, 0)] = col[0];
             a.out_img[img_index(a, tg.pix, b, 1)] = col[1];
@@ -929,7 +936,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
             // Fallback when the forward kernel ran out of record space: rebuild
             // the chunk's list and classify every pair again.
             int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
-                                             tg.cx1, tg.cy1, list[wave], lane)
+                                             tg.cx1, tg.cy1, list[wave], lane, F_TAPE)
                                 : 0;
             for (int i = 0; i < count; i++) {
                 const uint32_t ent = uniform_u32(list[wave][i]);
@@ -1106,6 +1113,12 @@ __global__ __launch_bounds__(256) void fit_tail(int iter, const float* __restric
     }
 }
 
+// Grid-stride fill with zeros.
+__global__ __launch_bounds__(256) void zero_floats(float* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+
 // ---------------------------------------------------------------- sRGB bytes
 
 // canvas.rs:100-105 encode_srgb, one value per thread: the byte is the number
@@ -1168,12 +1181,20 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
     return hipGetLastError();
 }
 
-hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int tape_mode,
-                        float* rec, float* zero_grads, hipStream_t s) {
-    int n = B * T;
+hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
+                        float* rec, float* zero_grads, hipStream_t s, const float* bg_src, float* bg_dst) {
+    const int n = B * T, n_bg = bg_dst ? 3 * B : 0;
+    const int threads = n > n_bg ? n : n_bg;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(setup_records, dim3((threads + 63) / 64), dim3(64), 0, s, params, n, W, H, sigma,
+                       setup_mode, rec, zero_grads, bg_src, bg_dst, n_bg);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero(float* p, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(setup_records, dim3((n + 63) / 64), dim3(64), 0, s, params, n, W, H, sigma,
-                       tape_mode, rec, zero_grads);
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(zero_floats, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 
@@ -1199,6 +1220,8 @@ hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t 
         return fast ? launch_forward_t<MODE_RENDER, true>(a, s) : launch_forward_t<MODE_RENDER, false>(a, s);
     if (mode == MODE_LOSS)
         return fast ? launch_forward_t<MODE_LOSS, true>(a, s) : launch_forward_t<MODE_LOSS, false>(a, s);
+    if (mode == MODE_RECORD)
+        return fast ? launch_forward_t<MODE_RECORD, true>(a, s) : launch_forward_t<MODE_RECORD, false>(a, s);
     return fast ? launch_forward_t<MODE_GRAD_IN, true>(a, s) : launch_forward_t<MODE_GRAD_IN, false>(a, s);
 }
 

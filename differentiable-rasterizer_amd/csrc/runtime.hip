@@ -250,9 +250,7 @@ int wait_stream(hipStream_t s) {
 
 // Argument checks shared by the raster entry points, with the reference
 // binding's messages (crates/diffrast-py/src/lib.rs:162-195).
-int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float sigma) {
-    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
-    if (!(std::isfinite(sigma) && sigma > 0.0f)) return fail(DRH_ERR_INVALID_ARG, "sigma must be positive and finite");
+int check_sizes(int64_t B, int64_t T, int64_t H, int64_t W) {
     if (B < 0 || T < 0 || H < 0 || W < 0) return fail(DRH_ERR_INVALID_ARG, "sizes must be non-negative");
     if (H == 0 || W == 0) return fail(DRH_ERR_INVALID_ARG, "height and width must be non-zero");
     if (B > 65535) return fail(DRH_ERR_TOO_LARGE, "batch of " + std::to_string(B) + " exceeds 65535 scenes per call");
@@ -260,6 +258,12 @@ int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float 
     if (T > (1 << 24)) return fail(DRH_ERR_TOO_LARGE, "more than 2^24 triangles per scene");
     if (B * T > (int64_t)INT32_MAX / 64) return fail(DRH_ERR_TOO_LARGE, "batch x triangles too large for one call");
     return DRH_OK;
+}
+
+int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float sigma) {
+    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
+    if (!(std::isfinite(sigma) && sigma > 0.0f)) return fail(DRH_ERR_INVALID_ARG, "sigma must be positive and finite");
+    return check_sizes(B, T, H, W);
 }
 
 struct Staged {
@@ -406,7 +410,8 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     }
     {
         KernelTimer kt(ctx, TK_SETUP, s);
-        HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma, mode != drh::MODE_RENDER, rec.get<float>(),
+        HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
+                                  mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, rec.get<float>(),
                                   mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s),
                 "setup_records launch");
     }
@@ -446,6 +451,47 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s),
                 "reduce_partials launch");
     }
+    return DRH_OK;
+}
+
+// The forward record that drh_render_record leaves for drh_backward_recorded,
+// in device memory the caller owns: the triangle records, a copy of the
+// backgrounds, the per-pixel hand-over and the per-tile entries (with their
+// counts), each starting at a 256-byte boundary.
+struct RecordLayout {
+    size_t rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, total = 0;
+    int cap2 = 0;
+};
+
+RecordLayout record_layout(int64_t B, int64_t T, int64_t H, int64_t W) {
+    RecordLayout L;
+    if (B == 0) return L;
+    const dim3 grid = drh::raster_grid((int)B, (int)W, (int)H);
+    const size_t ntiles = (size_t)B * grid.x * grid.y * drh::WAVES;
+    L.cap2 = tile_entries(ntiles, (int)T);
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t off = 0;
+    L.rec = off;
+    off = up(off + (size_t)B * T * drh::REC * sizeof(float));
+    L.bg = off;
+    off = up(off + (size_t)B * 3 * sizeof(float));
+    L.pstate = off;
+    off = up(off + (size_t)B * H * W * sizeof(drh::PixState));
+    L.tl_n = off;
+    off = up(off + ntiles * 2 * sizeof(int));
+    L.tl_ent = off;
+    off = up(off + ntiles * (size_t)L.cap2 * sizeof(drh::TileEnt));
+    L.total = off;
+    return L;
+}
+
+int check_record(const void* record, uint64_t record_bytes, const RecordLayout& L) {
+    if (!record) return fail(DRH_ERR_INVALID_ARG, "record is NULL");
+    if (record_bytes != L.total)
+        return fail(DRH_ERR_INVALID_ARG, "record of " + std::to_string(record_bytes) + " bytes; these sizes need " +
+                                             std::to_string(L.total) + " (drh_record_bytes)");
+    if (reinterpret_cast<uintptr_t>(record) % 256 != 0)
+        return fail(DRH_ERR_INVALID_ARG, "record must be 256-byte aligned");
     return DRH_OK;
 }
 
@@ -685,6 +731,118 @@ int drh_backward_from_grad(drh_ctx* ctx, const float* params, const float* backg
     if ((rc = run_raster(ctx, drh::MODE_GRAD_IN, p.dev, bg.dev, gi.dev, (int)B, (int)T, (int)H, (int)W, sigma,
                          nullptr, grads.dev, nullptr, flags, s)))
         return rc;
+    if ((rc = copy_back(grads, s))) return rc;
+    return finish(flags, s);
+}
+
+int drh_record_bytes(int64_t B, int64_t T, int64_t H, int64_t W, uint64_t* out_bytes) {
+    if (!out_bytes) return fail(DRH_ERR_INVALID_ARG, "out_bytes is NULL");
+    int rc = check_sizes(B, T, H, W);
+    if (rc) return rc;
+    *out_bytes = record_layout(B, T, H, W).total;
+    return DRH_OK;
+}
+
+int drh_render_record(drh_ctx* ctx, const float* params, const float* backgrounds, int64_t B, int64_t T,
+                      int64_t H, int64_t W, float sigma, float* out_images, void* record, uint64_t record_bytes,
+                      void* stream, uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (B == 0) return DRH_OK;
+    if (!out_images || !backgrounds) return fail(DRH_ERR_INVALID_ARG, "output or background pointer is NULL");
+    const RecordLayout L = record_layout(B, T, H, W);
+    if ((rc = check_record(record, record_bytes, L))) return rc;
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const bool host = flags & DRH_HOST_PTRS;
+    Staged p, bg;
+    Out img;
+    if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
+    char* base = static_cast<char*>(record);
+    drh::RasterArgs a{};
+    a.B = (int)B;
+    a.T = (int)T;
+    a.H = (int)H;
+    a.W = (int)W;
+    a.sigma = sigma;
+    a.rec = reinterpret_cast<float*>(base + L.rec);
+    a.bg = reinterpret_cast<float*>(base + L.bg);
+    a.out_img = img.dev;
+    a.pstate = reinterpret_cast<drh::PixState*>(base + L.pstate);
+    a.tl_ent = reinterpret_cast<drh::TileEnt*>(base + L.tl_ent);
+    a.cap2 = L.cap2;
+    a.tl_n = reinterpret_cast<int*>(base + L.tl_n);
+    a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
+    {
+        KernelTimer kt(ctx, TK_SETUP, s);
+        HIP_TRY(drh::launch_setup(p.dev, a.B, a.T, a.W, a.H, sigma, drh::SETUP_RECORD, const_cast<float*>(a.rec),
+                                  nullptr, s, bg.dev, const_cast<float*>(a.bg)),
+                "setup_records launch");
+    }
+    {
+        KernelTimer kt(ctx, TK_RASTER, s);
+        HIP_TRY(drh::launch_forward(drh::MODE_RECORD, !(flags & DRH_EXACT_MATH), a, s), "forward_kernel launch");
+    }
+    if ((rc = copy_back(img, s))) return rc;
+    return finish(flags, s);
+}
+
+int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_bytes, const float* grad_images,
+                          int64_t B, int64_t T, int64_t H, int64_t W, float sigma, float* out_grads, void* stream,
+                          uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (B == 0 || T == 0) return DRH_OK;
+    if (!out_grads) return fail(DRH_ERR_INVALID_ARG, "output pointer is NULL");
+    const RecordLayout L = record_layout(B, T, H, W);
+    if ((rc = check_record(record, record_bytes, L))) return rc;
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const bool host = flags & DRH_HOST_PTRS;
+    const bool det = (flags & DRH_DETERMINISTIC) != 0;
+    Staged gi;
+    Out grads;
+    Lease partials;
+    if ((rc = stage_in(ctx, gi, K_IN_IMAGES, grad_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = stage_out(ctx, grads, K_OUT_GRADS, out_grads, (size_t)B * T * NP, host, s))) return rc;
+    const dim3 grid = drh::raster_grid((int)B, (int)W, (int)H);
+    const int nblk = (int)(grid.x * grid.y);
+    if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s))) return rc;
+    const char* base = static_cast<const char*>(record);
+    drh::RasterArgs a{};
+    a.B = (int)B;
+    a.T = (int)T;
+    a.H = (int)H;
+    a.W = (int)W;
+    a.sigma = sigma;
+    a.rec = reinterpret_cast<const float*>(base + L.rec);
+    a.bg = reinterpret_cast<const float*>(base + L.bg);
+    a.grad_in = gi.dev;
+    a.partials = partials.get<float>();
+    // read only by the backward kernel; the casts follow RasterArgs' field types
+    a.pstate = reinterpret_cast<drh::PixState*>(const_cast<char*>(base + L.pstate));
+    a.tl_ent = reinterpret_cast<drh::TileEnt*>(const_cast<char*>(base + L.tl_ent));
+    a.cap2 = L.cap2;
+    a.tl_n = reinterpret_cast<int*>(const_cast<char*>(base + L.tl_n));
+    a.grads = grads.dev;
+    a.deterministic = det ? 1 : 0;
+    a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
+    if (!det) {
+        KernelTimer kt(ctx, TK_SETUP, s);
+        HIP_TRY(drh::launch_zero(grads.dev, (size_t)B * T * NP, s), "zero_floats launch");
+    }
+    {
+        KernelTimer kt(ctx, TK_BACKWARD, s);
+        HIP_TRY(drh::launch_backward(drh::MODE_GRAD_IN, !(flags & DRH_EXACT_MATH), L.cap2 < T, a, s),
+                "backward_kernel launch");
+    }
+    if (det) {
+        KernelTimer kt(ctx, TK_REDUCE, s);
+        HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, a.T, 3 * a.H * a.W, grads.dev, nullptr, s),
+                "reduce_partials launch");
+    }
     if ((rc = copy_back(grads, s))) return rc;
     return finish(flags, s);
 }

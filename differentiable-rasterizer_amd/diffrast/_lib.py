@@ -108,6 +108,11 @@ SIGNATURES = {
     "drh_fit_validate": ([ctypes.POINTER(FitConfig), _I64], ctypes.c_int),
     "drh_fit": ([_P, _P, _I64, _I64, _P, _P, _I64, ctypes.POINTER(FitConfig), _P, _P, _P,
                  ctypes.POINTER(FitReport), _P, _U32], ctypes.c_int),
+    "drh_record_bytes": ([_I64, _I64, _I64, _I64, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "drh_render_record": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, ctypes.c_uint64, _P, _U32],
+                          ctypes.c_int),
+    "drh_backward_recorded": ([_P, _P, ctypes.c_uint64, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _U32],
+                              ctypes.c_int),
     "drh_encode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
     "drh_decode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
 }
@@ -234,6 +239,18 @@ class Context:
         check(lib().drh_backward_from_grad(self.handle, params, bgs, grad_images, B, T, H, W, sigma,
                                            grads, stream, flags))
 
+    def render_record_ptr(self, params, bgs, B, T, H, W, sigma, out, record, record_bytes, stream=None,
+                          flags=0):
+        """drh_render that also fills `record` (record_bytes(B, T, H, W) bytes of device memory)."""
+        check(lib().drh_render_record(self.handle, params, bgs, B, T, H, W, sigma, out, record, record_bytes,
+                                      stream, flags))
+
+    def backward_recorded_ptr(self, record, record_bytes, grad_images, B, T, H, W, sigma, grads, stream=None,
+                              flags=0):
+        """Gradients for the scenes of a render_record_ptr call, from its record."""
+        check(lib().drh_backward_recorded(self.handle, record, record_bytes, grad_images, B, T, H, W, sigma,
+                                          grads, stream, flags))
+
     def encode_srgb_ptr(self, values, n, out, stream=None, flags=0):
         check(lib().drh_encode_srgb(self.handle, values, n, out, stream, flags))
 
@@ -331,6 +348,13 @@ def validate_fit_config(T: int, **cfg) -> str | None:
                      c["lr_alpha"], -1 if c["patience"] is None else c["patience"], c["min_delta"])
     rc = lib().drh_fit_validate(ctypes.byref(conf), T)
     return CONFIG_ERRORS.get(rc)
+
+
+def record_bytes(B: int, T: int, H: int, W: int) -> int:
+    """Device bytes drh_render_record keeps for B scenes of T triangles at H x W."""
+    n = ctypes.c_uint64()
+    check(lib().drh_record_bytes(B, T, H, W, ctypes.byref(n)))
+    return int(n.value)
 
 
 def params_per_triangle() -> int:

@@ -14,6 +14,10 @@ Same functions, argument meanings and ValueError cases as the reference
   copies every call to CPU numpy, torch_layer.py:46, 58-59, 123-124).
   CPU tensors are moved to the current GPU and results are returned on the
   caller's device, as the reference returns them.
+* When autograd will need it, `rasterize` keeps its forward pass's record
+  (a device tensor of `_lib.record_bytes(B, T, H, W)` bytes, held until the
+  graph is freed) and its backward runs only the backward kernel; the
+  reference's backward renders the batch again (torch_layer.py:55-66).
 * There is no CPU backend. `device="gpu"`, `"cuda"` and `"auto"` run the HIP
   kernels; `device="cpu"` raises ValueError instead of silently running
   something else, and a missing library or GPU raises rather than falling
@@ -126,35 +130,63 @@ def _render(params: Tensor, height: int, width: int, sigma: float, background, c
     return out
 
 
+def _render_record(params: Tensor, height: int, width: int, sigma: float, background,
+                   channels_first: bool) -> tuple[Tensor, Tensor]:
+    """_render that also returns the forward record the backward pass reads."""
+    dev = _gpu()
+    p = _on_gpu(params, dev)
+    B, T = p.shape[0], p.shape[1]
+    bg = _backgrounds(background, B, dev)
+    shape = (B, 3, height, width) if channels_first else (B, height, width, 3)
+    out = torch.empty(shape, device=dev, dtype=torch.float32)
+    nbytes = _lib.record_bytes(B, T, height, width)
+    record = torch.empty((nbytes,), device=dev, dtype=torch.uint8)
+    _context(dev).render_record_ptr(p.data_ptr(), bg.data_ptr(), B, T, height, width, float(sigma),
+                                    out.data_ptr(), record.data_ptr(), nbytes, _stream(dev),
+                                    _lib.CHANNELS_FIRST if channels_first else 0)
+    _note_gpu()
+    return out, record
+
+
 class _Rasterize(torch.autograd.Function):
-    """Forward renders, backward maps dL/dimage to dL/dparams (torch_layer.py:37-66)."""
+    """Forward renders, backward maps dL/dimage to dL/dparams (torch_layer.py:36-66)."""
 
     @staticmethod
     def forward(ctx, params: Tensor, height: int, width: int, sigma: float, background, device,
-                channels_first: bool):
-        images = _render(params, height, width, sigma, background, channels_first)
-        ctx.save_for_backward(params)
+                channels_first: bool, keep_record: bool):
+        if keep_record:
+            images, record = _render_record(params, height, width, sigma, background, channels_first)
+            ctx.save_for_backward(params, record)
+        else:
+            images = _render(params, height, width, sigma, background, channels_first)
+            ctx.save_for_backward(params)
         ctx.sigma = sigma
         ctx.background = background
         ctx.device = device
         ctx.channels_first = channels_first
+        ctx.size = (height, width)
         return images
 
     @staticmethod
     def backward(ctx, grad_images: Tensor):
-        (params,) = ctx.saved_tensors
+        params, *kept = ctx.saved_tensors
         dev = _gpu()
-        p = _on_gpu(params, dev)
         g = _on_gpu(grad_images, dev)
-        B, T = p.shape[0], p.shape[1]
-        H, W = (g.shape[2], g.shape[3]) if ctx.channels_first else (g.shape[1], g.shape[2])
-        bg = _backgrounds(ctx.background, B, dev)
+        B, T = params.shape[0], params.shape[1]
+        H, W = ctx.size
+        flags = _lib.CHANNELS_FIRST if ctx.channels_first else 0
         grads = torch.empty((B, T, N_PARAMS), device=dev, dtype=torch.float32)
-        _context(dev).from_grad_ptr(p.data_ptr(), bg.data_ptr(), g.data_ptr(), B, T, H, W,
-                                    float(ctx.sigma), grads.data_ptr(), _stream(dev),
-                                    _lib.CHANNELS_FIRST if ctx.channels_first else 0)
+        if kept:
+            (record,) = kept
+            _context(dev).backward_recorded_ptr(record.data_ptr(), record.numel(), g.data_ptr(), B, T, H, W,
+                                                float(ctx.sigma), grads.data_ptr(), _stream(dev), flags)
+        else:
+            p = _on_gpu(params, dev)
+            bg = _backgrounds(ctx.background, B, dev)
+            _context(dev).from_grad_ptr(p.data_ptr(), bg.data_ptr(), g.data_ptr(), B, T, H, W,
+                                        float(ctx.sigma), grads.data_ptr(), _stream(dev), flags)
         _note_gpu()
-        return grads.to(params.device, params.dtype), None, None, None, None, None, None
+        return grads.to(params.device, params.dtype), None, None, None, None, None, None, None
 
 
 def rasterize(
@@ -189,7 +221,9 @@ def rasterize(
     _check_sigma(sigma)
     _parse_device(device)
 
-    images = _Rasterize.apply(params, height, width, sigma, background, device, bool(channels_first))
+    keep_record = torch.is_grad_enabled() and params.requires_grad
+    images = _Rasterize.apply(params, height, width, sigma, background, device, bool(channels_first),
+                              keep_record)
     return images.to(params.device, params.dtype)
 
 

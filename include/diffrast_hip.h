@@ -123,6 +123,34 @@ int drh_backward_from_grad(drh_ctx *ctx, const float *params, const float *backg
                            const float *grad_images, int64_t B, int64_t T, int64_t H, int64_t W,
                            float sigma, float *out_grads, void *stream, uint32_t flags);
 
+/* A render kept for its backward pass. The reference has no counterpart: its
+ * PyTorch op renders in forward (python/diffrast/torch_layer.py:40-52) and its
+ * backward re-renders the batch (torch_layer.py:55-66 via backward_batch,
+ * crates/diffrast-py/src/lib.rs:245-324). Here the forward keeps, in device
+ * memory the caller owns, what the backward kernel reads (triangle records,
+ * backgrounds, per-pixel transmittance, per-tile entry lists), so the backward
+ * runs only the backward kernel.
+ *
+ * drh_record_bytes gives the size of that memory for B x T triangles at H x W
+ * (0 when B == 0). */
+int drh_record_bytes(int64_t B, int64_t T, int64_t H, int64_t W, uint64_t *out_bytes);
+
+/* drh_render that also fills `record` (device memory, 256-byte aligned, of
+ * exactly drh_record_bytes(B, T, H, W) bytes). The image is drh_render's, bit
+ * for bit. The record stays valid until the caller frees or overwrites it;
+ * params and backgrounds are not needed afterwards. */
+int drh_render_record(drh_ctx *ctx, const float *params, const float *backgrounds, int64_t B, int64_t T,
+                      int64_t H, int64_t W, float sigma, float *out_images, void *record,
+                      uint64_t record_bytes, void *stream, uint32_t flags);
+
+/* drh_backward_from_grad for the scenes of a drh_render_record call, from its
+ * record, without rendering again: B, T, H, W, sigma and DRH_EXACT_MATH must be
+ * those of that call (DRH_CHANNELS_FIRST here describes grad_images). The
+ * record is only read, so one record serves any number of backward calls. */
+int drh_backward_recorded(drh_ctx *ctx, const void *record, uint64_t record_bytes,
+                          const float *grad_images, int64_t B, int64_t T, int64_t H, int64_t W,
+                          float sigma, float *out_grads, void *stream, uint32_t flags);
+
 /* One Adam step (optim.rs:40-60) over n parameters with per-parameter
  * learning rates, then fit.rs:399-424 project() when `project` is nonzero
  * (n must then be a multiple of 10). `step` is the step count after the

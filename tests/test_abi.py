@@ -71,3 +71,34 @@ def test_create_reports_no_device_without_a_gpu(L):
     h = ctypes.c_void_p()
     assert L.lib().drh_create(ctypes.byref(h)) == 1  # NoAdapter
     assert "no HIP device" in L.last_error()
+
+
+def test_record_bytes_cover_every_part(L):
+    # host-only sizing of the forward record: triangle records (76 floats each),
+    # backgrounds, 24 bytes per pixel, two counts per tile and T entries of 24 bytes
+    # per 8x8 tile, each part rounded up to 256 bytes
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    B, T, H, W = 16, 128, 256, 256
+    tiles = B * (W // 8) * (H // 8)
+    want = up(B * T * 76 * 4) + up(B * 3 * 4) + up(B * H * W * 24) + up(tiles * 8) + up(tiles * T * 24)
+    assert L.record_bytes(B, T, H, W) == want
+    assert L.record_bytes(0, T, H, W) == 0
+    # odd sizes count the partial tiles of whole 16x16 blocks
+    tiles = 3 * 2 * 2 * 4  # 2 x 2 blocks of 2 x 2 tiles per scene
+    assert L.record_bytes(3, 5, 17, 30) == (up(3 * 5 * 76 * 4) + up(36) + up(3 * 17 * 30 * 24) + up(tiles * 8)
+                                           + up(tiles * 5 * 24))
+    with pytest.raises(L.DiffrastError) as e:
+        L.record_bytes(1, 1, 0, 4)
+    assert e.value.code == 6
+
+
+def test_record_keeps_a_bounded_number_of_entries(L, monkeypatch):
+    # past 1 GiB of entries the record keeps as many per tile as fit (at least 128)
+    B, T, H, W = 16, 4096, 512, 512
+    tiles = B * (W // 8) * (H // 8)
+    cap = (1 << 30) // (tiles * 24)
+    assert cap >= 128
+    n = L.record_bytes(B, T, H, W)
+    assert n - (1 << 30) < B * T * 76 * 4 + B * H * W * 24 + tiles * 8 + 4096
+    monkeypatch.setenv("DRH_MAX_TILE_ENTRIES", "7")
+    assert L.record_bytes(2, 50, 16, 16) < L.record_bytes(2, 7, 16, 16) + 2 * 50 * 76 * 4
