@@ -29,6 +29,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -455,7 +456,10 @@ __device__ inline uint64_t uniform_u64(uint64_t v) {
     return ((uint64_t)uniform_u32((uint32_t)(v >> 32)) << 32) | (uint64_t)uniform_u32((uint32_t)v);
 }
 
-__device__ inline void lds_add(float* p, float v) {
+// A pointer into LDS: 32-bit addresses (a generic pointer is 64-bit).
+typedef __attribute__((address_space(3))) float lds_float;
+
+__device__ inline void lds_add(lds_float* p, float v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
@@ -607,13 +611,17 @@ struct Trans {
     int e;    // number of 2^64 rescalings applied to q
 };
 
+__device__ inline void trans_rescale(Trans& t) {
+    const bool small = t.q < 5.421010862427522e-20f;  // 2^-64
+    t.q = small ? t.q * 1.8446744073709552e19f : t.q;  // 2^64
+    t.e += small ? 1 : 0;
+}
+
 __device__ inline void trans_mul(Trans& t, float f) {
     const bool zero = f == 0.0f;
-    float q = zero ? t.q : t.q * f;
-    const bool small = q < 5.421010862427522e-20f;  // 2^-64
-    t.q = small ? q * 1.8446744073709552e19f : q;   // 2^64
-    t.e += small ? 1 : 0;
+    t.q = zero ? t.q : t.q * f;
     t.z += zero ? 1 : 0;
+    trans_rescale(t);
 }
 
 // prod_{j>k} (1 - w_j) from the totals and the prefix through k.
@@ -642,7 +650,7 @@ struct TileGeo {
 __device__ inline TileGeo tile_geo(int W, int H) {
     TileGeo t;
     t.lane = threadIdx.x & 63;
-    t.wave = threadIdx.x >> 6;
+    t.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile indices
     t.b = blockIdx.z;
     t.tx0 = (blockIdx.x * 2 + (t.wave & 1)) * TILE;
     t.ty0 = (blockIdx.y * 2 + (t.wave >> 1)) * TILE;
@@ -695,7 +703,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     int n2 = 0;                 // contributing entries seen (recorded while n2 < cap2)
     int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
     const int cap2 = a.cap2;
-    TileEnt* te = a.tl_ent + tg.tile * cap2;
+    // wave-uniform: the entry stores address from a scalar base
+    TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -798,18 +807,30 @@ struct Back {
 // chain is predicated rather than branched: in the backward every entry has
 // contributing lanes, so a branch would never skip. `any_band` (wave-uniform)
 // skips the vertex terms when no lane took the exact path.
+// PLAIN: no pixel of the wave met a zero factor or a rescaling in the forward
+// pass (its totals have z == e == 0). The prefixes of a pixel's product are at
+// least its total, so none of them needs either, and the transmittance is a
+// plain product: trans_mul and trans_suffix then give these same values.
+template <bool PLAIN>
 __device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_band, float w, float cov,
                                   const Geo& g, Pix p, float rsig, Back& st, float (&a)[NP]) {
     const float omw = 1.0f - w;
-    trans_mul(st.pre, on ? omw : 1.0f);
     // d_canvas as the reference holds it at layer k: g0 prod_{j>k} (1 - w_j)
-    const float tk = on ? trans_suffix(st.tot, st.pre) : 0.0f;
+    float tk;
+    if (PLAIN) {
+        st.pre.q = on ? st.pre.q * omw : st.pre.q;
+        tk = on ? st.tot.q * __builtin_amdgcn_rcpf(st.pre.q) : 0.0f;
+    } else {
+        trans_mul(st.pre, on ? omw : 1.0f);
+        tk = on ? trans_suffix(st.tot, st.pre) : 0.0f;
+    }
     const float tw = tk * w;
     float sw = 0.0f;
     for (int ch = 0; ch < 3; ch++) {
         a[6 + ch] = st.g0[ch] * tw;
-        sw = fmaf(st.g0[ch], r.f(R_C + ch) - st.col[ch], sw);
-        const float o = fmaf(r.f(R_C + ch), w, st.col[ch] * omw);
+        const float d = r.f(R_C + ch) - st.col[ch];
+        sw = fmaf(st.g0[ch], d, sw);
+        const float o = fmaf(w, d, st.col[ch]);  // col + w (c - col)
         st.col[ch] = on ? o : st.col[ch];
     }
     const float d_w = tk * sw;
@@ -846,13 +867,17 @@ __device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_ban
 // of the per-wave accumulator. Within a wave the entries are sequential, so
 // each accumulator receives its adds in list order: the sums are reproducible
 // run to run. `any_band` (wave-uniform) says whether any vertex term is set.
-__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, float* dst, int lane, int p10) {
+// `slot10` and `slot4` are this lane's accumulator addresses for the 10- and
+// 4-value sums in the row of the first triangle of the chunk; `row` (uniform)
+// is the triangle's row offset.
+__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, int row, lds_float* slot10,
+                                    lds_float* slot4, int lane, int p10) {
     if (any_band) {
         float e = wave_reduce10(a, lane);
-        if (p10 >= 0) lds_add(dst + p10, e);
+        if (p10 >= 0) lds_add(slot10 + row, e);
     } else {
         float e = wave_reduce4(a[6], a[7], a[8], a[9]);
-        if ((lane & 15) == 0) lds_add(dst + 6 + (lane >> 4), e);
+        if ((lane & 15) == 0) lds_add(slot4 + row, e);
     }
 }
 
@@ -900,7 +925,39 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     const size_t blk = tg.tile / WAVES;
     float* accw = acc[wave];
     const int p10 = red10_param(lane);
+    lds_float* const slot10 = (lds_float*)accw + (p10 >= 0 ? p10 : 0);
+    lds_float* const slot4 = (lds_float*)accw + 6 + (lane >> 4);
     int i2 = 0;
+    const bool plain = __ballot(st.tot.z != 0 || st.tot.e != 0) == 0;
+
+    // The entries the forward kernel recorded: which lanes contribute and
+    // which of them took the exact path are known; only w is recomputed. The
+    // next entry is read one iteration ahead.
+    auto recorded = [&](auto plain_c, int k0, int k1) {
+        constexpr bool PLAIN = decltype(plain_c)::value;
+        TileEnt nx = te[min(i2, cap2 - 1)];
+        for (; i2 < n2r; i2++) {
+            const TileEnt cur = nx;
+            const int k = (int)(cur.k >> 8);
+            if (k >= k1) break;
+            nx = te[min(i2 + 1, cap2 - 1)];
+            const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
+            const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
+            const float* rp = rec + (size_t)k * REC;
+            const Rec r = load_rec(rp);
+            float cov = 1.0f;
+            Geo g;
+            if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            const float w = r.f(R_A) * cov;
+            float part[NP];
+            grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
+            // the row offset by the scalar unit: the compiler would fold it into a
+            // 64-bit multiply-add on the vector unit
+            int row;
+            asm("s_mul_i32 %0, %1, %2" : "=s"(row) : "s"(__builtin_amdgcn_readfirstlane(k - k0)), "n"(NP));
+            reduce_entry(part, cur.band != 0, row, slot10, slot4, lane, p10);
+        }
+    };
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -911,27 +968,10 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
         if (c < rec_chunks) {
-            // The entries the forward kernel recorded: which lanes contribute
-            // and which of them took the exact path are known; only w is
-            // recomputed. The next entry is read one iteration ahead.
-            TileEnt nx = te[min(i2, cap2 - 1)];
-            for (; i2 < n2r; i2++) {
-                const TileEnt cur = nx;
-                const int k = (int)(cur.k >> 8);
-                if (k >= k1) break;
-                nx = te[min(i2 + 1, cap2 - 1)];
-                const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
-                const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
-                const float* rp = rec + (size_t)k * REC;
-                const Rec r = load_rec(rp);
-                float cov = 1.0f;
-                Geo g;
-                if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
-                const float w = r.f(R_A) * cov;
-                float part[NP];
-                grad_pixel(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, cur.band != 0, accw + (k - k0) * NP, lane, p10);
-            }
+            if (plain)
+                recorded(std::true_type{}, k0, k1);
+            else
+                recorded(std::false_type{}, k0, k1);
         } else if (REBUILD) {
             // Fallback when the forward kernel ran out of record space: rebuild
             // the chunk's list and classify every pair again.
@@ -951,8 +991,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                 const bool any_band = __ballot(on && band) != 0;
                 band = band && on;
                 float part[NP];
-                grad_pixel(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, any_band, accw + kl * NP, lane, p10);
+                grad_pixel<false>(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
+                reduce_entry(part, any_band, kl * NP, slot10, slot4, lane, p10);
             }
         }
         __syncthreads();

@@ -134,6 +134,31 @@ def test_opaque_stack_and_clamped_alpha(ctx, orc):
     assert pinned.sum() > 10 and np.all(gg[..., 9][pinned] == 0.0)
 
 
+def test_deep_stack_rescales_the_transmittance(ctx, orc):
+    # 70 large triangles of alpha 0.8-0.95: where ~25 or more cover a pixel its
+    # transmittance falls below 2^-64 and the kernels rescale it (10 and 6 of the
+    # 30 tiles; those take the general transmittance path, the others the plain product)
+    rng = np.random.default_rng(5)
+    B, T, H, W = 2, 70, 40, 48
+    ang = rng.uniform(0, 2 * np.pi, (B, T, 3))
+    rad = rng.uniform(0.9, 1.6, (B, T, 3))
+    params = np.zeros((B, T, 10), np.float32)
+    params[..., 0:6:2] = 0.5 + rad * np.cos(ang)
+    params[..., 1:6:2] = 0.5 + rad * np.sin(ang)
+    params[..., 6:9] = rng.uniform(0, 1, (B, T, 3))
+    params[..., 9] = rng.uniform(0.8, 0.95, (B, T))
+    params[1, :, :6] = params[1, :, :6] * 0.5 + 0.25
+    targets = np.stack([synth.blob_target(7 + b, H, W) for b in range(B)])
+    for sigma in (0.003, 0.02):
+        gl, gg = ctx.fused_loss_backward(params, targets, sigma)
+        cl, cg = orc.loss_backward_batch(params, targets, sigma)
+        check_losses(gl, cl)
+        assert grad_err(gg, cg) <= GRAD_RTOL
+        gi = (targets - 0.5).astype(np.float32) * 1e-3
+        assert grad_err(ctx.backward_from_grad(params, gi, sigma),
+                        orc.backward_from_grad_batch(params, gi, sigma)) <= GRAD_RTOL
+
+
 def test_special_triangles(ctx, orc):
     nan = float("nan")
     params = synth.batch("uniform", 1, 12, 11)
