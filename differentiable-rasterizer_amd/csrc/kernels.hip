@@ -541,9 +541,16 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                         // The reference's rounded distances are within ~1e-7 (1 + max |v|)
                         // of these bounds' exact values; 0.1 slack is ten times that.
                         const float lim = ubmin + 0.1f * slack;
+                        // An edge farther than `sat` from every pixel is nearest only
+                        // where the pair saturates (coverage exactly 1 inside, w below
+                        // MIN_WEIGHT outside: deep and far include the slack), and there
+                        // the plan's edge, no nearer, saturates alike. It is no candidate
+                        // unless it is the closest.
+                        const float sat = fmaxf(far, -deep);
+                        const float lbmin = fminf(fminf(lb[0], lb[1]), lb[2]);
                         int ncand = 0, jc = 0;
                         for (int j = 0; j < 3; j++)
-                            if (!(lb[j] > lim)) {
+                            if (!(lb[j] > lim) && (lb[j] <= sat || lb[j] == lbmin)) {
                                 ncand++;
                                 jc = j;
                             }
