@@ -60,7 +60,7 @@ constexpr int CAP2_MIN = 128;
 // (with scalar loads) by the backward kernel.
 struct TileEnt {
     uint32_t k;     // (k << 8) | (plan << 2) | class, k the triangle index
-    uint32_t pad;
+    uint32_t row;   // byte offset of the triangle's row in a chunk's per-wave accumulator
     uint64_t on;    // lanes with w > MIN_WEIGHT
     uint64_t band;  // of those, lanes on the exact path
 };
@@ -72,6 +72,15 @@ struct PixState {
     float q;      // total transmittance: product of the nonzero (1 - w),
     int z, e;     // the count of zero factors and of 2^64 rescalings of q
 };
+
+// The raster kernels' block order, made by setup_records (perm null: none):
+// perm[b * gx*gy + r] is the scene-local index of scene b's r-th heaviest block;
+// gx, gy: blocks per scene row and column, (gx + 1) * (gy + 1) <= ORD_MAX_CELLS.
+struct OrderArgs {
+    int* perm;
+    int gx, gy;
+};
+constexpr int ORD_MAX_CELLS = 8192;
 
 struct RasterArgs {
     int B, T, H, W;
@@ -91,6 +100,8 @@ struct RasterArgs {
     float* losses;         // B (MODE_LOSS)
     int deterministic;     // per-block partial rows + reduce_partials instead of atomics
     int chw;               // images, targets and grad_in are B x 3 x H x W (else B x H x W x 3)
+    const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
+    const int* perm_bwd;   // block order of the backward kernel or null
 };
 
 // Device-side state of a running fit (fit.rs:197-211).
@@ -109,10 +120,11 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
                            float min_delta, long long patience, FitState* st, float* losses_out,
                            float* best_params, hipStream_t s);
 
-// bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src.
+// bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src; with
+// o.cnt, the block order is made (OrderArgs).
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
                         float* rec, float* zero_grads, hipStream_t s, const float* bg_src = nullptr,
-                        float* bg_dst = nullptr);
+                        float* bg_dst = nullptr, const OrderArgs& o = OrderArgs{});
 // n floats set to zero by a kernel (no memset node, so callers may capture it).
 hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);

@@ -57,19 +57,40 @@ __device__ inline int upper_bound_px(float hi, float pad, int n) {
     return (c >= (float)n) ? n : (int)c + 1;
 }
 
-__global__ void setup_records(const float* __restrict__ params, int n_tri, int W, int H,
-                              float sigma, int setup_mode, float* __restrict__ rec,
-                              float* __restrict__ zero_grads, const float* __restrict__ bg_src,
-                              float* __restrict__ bg_dst, int n_bg) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    // A record kept for a later backward holds its own copy of the backgrounds.
-    if (bg_dst && i < n_bg) bg_dst[i] = bg_src[i];
-    if (i >= n_tri) return;
+// A triangle's cull box in 16x16 blocks (inclusive; x0 > x1 when empty).
+struct BlockBox {
+    int x0, y0, x1, y1;
+};
+
+// The box of triangle p as setup_one makes it (raster.rs:26-28, 144-168), for
+// the block-order estimate of another workgroup than the one that sets it up.
+__device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, float sigma) {
+    float v[6];
+    bool finite = true;
+    for (int j = 0; j < 6; j++) {
+        v[j] = p[j];
+        finite = finite && isfinite(v[j]);
+    }
+    BlockBox bb = {1, 1, 0, 0};
+    if (!finite || !(p[9] > 0.0f)) return bb;
+    const float pad = 6.0f * sigma;
+    const int bx0 = lower_bound_px(fminf(fminf(v[0], v[2]), v[4]), pad, W);
+    const int by0 = lower_bound_px(fminf(fminf(v[1], v[3]), v[5]), pad, H);
+    const int bx1 = upper_bound_px(fmaxf(fmaxf(v[0], v[2]), v[4]), pad, W);
+    const int by1 = upper_bound_px(fmaxf(fmaxf(v[1], v[3]), v[5]), pad, H);
+    if (bx0 < bx1 && by0 < by1) bb = {bx0 >> 4, by0 >> 4, (bx1 - 1) >> 4, (by1 - 1) >> 4};
+    return bb;
+}
+
+// Setup of triangle i (scene-major index): its record, and its box in blocks
+// (empty when the triangle is not drawn).
+__device__ inline BlockBox setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
+                                     int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
     // The backward kernel adds into the gradients: they start at zero.
     if (zero_grads)
-        for (int j = 0; j < NP; j++) zero_grads[(size_t)i * NP + j] = 0.0f;
-    const float* p = params + (size_t)i * NP;
-    float* r = rec + (size_t)i * REC;
+        for (int j = 0; j < NP; j++) zero_grads[i * NP + j] = 0.0f;
+    const float* p = params + i * NP;
+    float* r = rec + i * REC;
 
     float v[6];
     for (int j = 0; j < 6; j++) v[j] = p[j];
@@ -179,6 +200,102 @@ __global__ void setup_records(const float* __restrict__ params, int n_tri, int W
         eb[6] = 0.0f;
         eb[7] = 0.0f;
     }
+    BlockBox bb = {1, 1, 0, 0};
+    if (live) bb = {bx0 >> 4, by0 >> 4, (bx1 - 1) >> 4, (by1 - 1) >> 4};
+    return bb;
+}
+
+// The raster kernels' block order, heaviest first. A block's time follows its
+// tiles' lists; the longest blocks, started late in a grid of several rounds,
+// run on while most of the device has nothing left, and heavy blocks that land
+// on one CU finish last. A block's cost is estimated by the number of triangle
+// boxes that overlap it plus a share for building its lists (which reads every
+// triangle). Each scene's workgroup counts the overlaps in LDS (a 2D difference
+// grid: four adds per triangle, then prefix sums along rows and columns),
+// counting-sorts the scene's blocks by the estimate, heaviest first, and writes
+// their scene-local indices to perm[b * nb ...]. The raster kernels take launch
+// slot i to rank i / B of scene i % B, so the heaviest blocks of every scene go
+// first. Nothing crosses workgroups: a device-wide hand-off would cost more
+// than the order saves.
+constexpr int SETUP_THREADS = 256, ORD_BUCKETS = 1024;
+
+__device__ inline void order_scene(const OrderArgs& o, int* cells, int b, int T) {
+    __shared__ int hist[ORD_BUCKETS];
+    __shared__ int scan[SETUP_THREADS];
+    const int t = threadIdx.x, gx = o.gx, gy = o.gy, pitch = gx + 1, nb = gx * gy;
+    for (int y = t; y <= gy; y += SETUP_THREADS) {
+        int run = 0;
+        for (int x = 0; x <= gx; x++) run = (cells[y * pitch + x] += run);
+    }
+    for (int k = t; k < ORD_BUCKETS; k += SETUP_THREADS) hist[k] = 0;
+    __syncthreads();
+    for (int x = t; x <= gx; x += SETUP_THREADS) {
+        int run = 0;
+        for (int y = 0; y <= gy; y++) run = (cells[y * pitch + x] += run);
+    }
+    __syncthreads();
+    const int base = 6 * ((T + 63) / 64);  // list building, against one overlapping box
+    auto key = [&](int blk) {
+        const int c = cells[(blk / gx) * pitch + blk % gx] + base;
+        return ORD_BUCKETS - 1 - min(c, ORD_BUCKETS - 1);
+    };
+    for (int blk = t; blk < nb; blk += SETUP_THREADS) atomicAdd(&hist[key(blk)], 1);
+    __syncthreads();
+    // exclusive prefix of the histogram: four buckets per thread, then a scan of
+    // the partial sums (Hillis-Steele in place)
+    constexpr int PER = ORD_BUCKETS / SETUP_THREADS;
+    int part = 0;
+    for (int q = 0; q < PER; q++) part += hist[t * PER + q];
+    scan[t] = part;
+    __syncthreads();
+    for (int off = 1; off < SETUP_THREADS; off <<= 1) {
+        const int add = t >= off ? scan[t - off] : 0;
+        __syncthreads();
+        scan[t] += add;
+        __syncthreads();
+    }
+    int run = scan[t] - part;
+    for (int q = 0; q < PER; q++) {
+        const int c = hist[t * PER + q];
+        hist[t * PER + q] = run;
+        run += c;
+    }
+    __syncthreads();
+    for (int blk = t; blk < nb; blk += SETUP_THREADS) o.perm[(size_t)b * nb + atomicAdd(&hist[key(blk)], 1)] = blk;
+}
+
+// Workgroup (x, b): the records of scene b's triangles [x n, x n + n), n the
+// workgroup size, and, for x == 0 with o.perm (then n == SETUP_THREADS), the
+// scene's block order from all its boxes (those of the other workgroups'
+// triangles are computed again here, which is cheap).
+__global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __restrict__ params, int T, int W,
+                                                               int H, float sigma, int setup_mode,
+                                                               float* __restrict__ rec, float* __restrict__ zero_grads,
+                                                               const float* __restrict__ bg_src,
+                                                               float* __restrict__ bg_dst, OrderArgs o) {
+    __shared__ int cells[ORD_MAX_CELLS];
+    const int b = blockIdx.y, k = blockIdx.x * blockDim.x + threadIdx.x, pitch = o.gx + 1;
+    const bool order = o.perm && blockIdx.x == 0;
+    // A record kept for a later backward holds its own copy of the backgrounds.
+    if (bg_dst && blockIdx.x == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
+    if (order) {
+        for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
+        __syncthreads();
+    }
+    BlockBox bb = {1, 1, 0, 0};
+    if (k < T) bb = setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
+    if (!order) return;
+    for (int q = threadIdx.x; q < T; q += SETUP_THREADS) {
+        if (q >= SETUP_THREADS) bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma);
+        if (bb.x0 <= bb.x1 && bb.y0 <= bb.y1) {
+            atomicAdd(&cells[bb.y0 * pitch + bb.x0], 1);
+            atomicAdd(&cells[bb.y0 * pitch + bb.x1 + 1], -1);
+            atomicAdd(&cells[(bb.y1 + 1) * pitch + bb.x0], -1);
+            atomicAdd(&cells[(bb.y1 + 1) * pitch + bb.x1 + 1], 1);
+        }
+    }
+    __syncthreads();
+    order_scene(o, cells, b, T);
 }
 
 // ---------------------------------------------------------------- per-pair math
@@ -647,20 +764,32 @@ __device__ inline size_t img_index(const RasterArgs& a, size_t pix, int b, int c
 // Tile geometry shared by both kernels: one wave per 8x8 tile, four tiles
 // (2x2) per block, one pixel per lane.
 struct TileGeo {
-    int lane, wave, b, x, y, tx0, ty0, tx1, ty1;
+    int lane, wave, b, bx, by, x, y, tx0, ty0, tx1, ty1;
     bool valid, live;
     Pix p;
     float cx0, cy0, cx1, cy1;
     size_t pix, tile;
 };
 
-__device__ inline TileGeo tile_geo(int W, int H) {
+// With `perm` (setup_records' block order of B scenes) launch slot i (scene-major
+// linear index) works on block perm[s * nb + i / B] of scene s = i % B.
+__device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int B = 1) {
     TileGeo t;
     t.lane = threadIdx.x & 63;
     t.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile indices
+    t.bx = blockIdx.x;
+    t.by = blockIdx.y;
     t.b = blockIdx.z;
-    t.tx0 = (blockIdx.x * 2 + (t.wave & 1)) * TILE;
-    t.ty0 = (blockIdx.y * 2 + (t.wave >> 1)) * TILE;
+    if (perm) {
+        const int nb = (int)(gridDim.x * gridDim.y);
+        const int i = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        t.b = i % B;
+        const int local = min(max(perm[(size_t)t.b * nb + i / B], 0), nb - 1);
+        t.bx = local % (int)gridDim.x;
+        t.by = local / (int)gridDim.x;
+    }
+    t.tx0 = (t.bx * 2 + (t.wave & 1)) * TILE;
+    t.ty0 = (t.by * 2 + (t.wave >> 1)) * TILE;
     t.x = t.tx0 + (t.lane & 7);
     t.y = t.ty0 + (t.lane >> 3);
     t.valid = t.x < W && t.y < H;
@@ -676,7 +805,7 @@ __device__ inline TileGeo tile_geo(int W, int H) {
     t.cx1 = ((float)(t.tx1 - 1) + 0.5f) / (float)W;
     t.cy1 = ((float)(t.ty1 - 1) + 0.5f) / (float)H;
     t.pix = ((size_t)t.b * H + (t.valid ? t.y : 0)) * W + (t.valid ? t.x : 0);
-    t.tile = (((size_t)t.b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * WAVES + t.wave;
+    t.tile = (((size_t)t.b * gridDim.y + t.by) * gridDim.x + t.bx) * WAVES + t.wave;
     return t;
 }
 
@@ -694,7 +823,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     __shared__ uint32_t list[WAVES][CH];
     __shared__ double loss[WAVES];
     const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo(W, H);
+    const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -748,7 +877,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                     if (n2 < cap2 && lane == 0) {
                         TileEnt e;
                         e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
-                        e.pad = 0;
+                        e.row = (ent >> 8) * (uint32_t)(NP * sizeof(float));
                         e.on = onm;
                         e.band = bm;
                         te[n2] = e;
@@ -875,16 +1004,17 @@ __device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_ban
 // each accumulator receives its adds in list order: the sums are reproducible
 // run to run. `any_band` (wave-uniform) says whether any vertex term is set.
 // `slot10` and `slot4` are this lane's accumulator addresses for the 10- and
-// 4-value sums in the row of the first triangle of the chunk; `row` (uniform)
-// is the triangle's row offset.
-__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, int row, lds_float* slot10,
+// 4-value sums in the row of the first triangle of the chunk; `row_bytes`
+// (uniform) is the triangle's row offset in bytes.
+__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, int row_bytes, lds_float* slot10,
                                     lds_float* slot4, int lane, int p10) {
+    typedef __attribute__((address_space(3))) char lds_char;
     if (any_band) {
         float e = wave_reduce10(a, lane);
-        if (p10 >= 0) lds_add(slot10 + row, e);
+        if (p10 >= 0) lds_add((lds_float*)((lds_char*)slot10 + row_bytes), e);
     } else {
         float e = wave_reduce4(a[6], a[7], a[8], a[9]);
-        if ((lane & 15) == 0) lds_add(slot4 + row, e);
+        if ((lane & 15) == 0) lds_add((lds_float*)((lds_char*)slot4 + row_bytes), e);
     }
 }
 
@@ -903,7 +1033,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     __shared__ uint32_t list[WAVES][CH];
     __shared__ float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo(W, H);
+    const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -958,11 +1088,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
-            // the row offset by the scalar unit: the compiler would fold it into a
-            // 64-bit multiply-add on the vector unit
-            int row;
-            asm("s_mul_i32 %0, %1, %2" : "=s"(row) : "s"(__builtin_amdgcn_readfirstlane(k - k0)), "n"(NP));
-            reduce_entry(part, cur.band != 0, row, slot10, slot4, lane, p10);
+            // the recorded byte offset: one add to this lane's address (the product
+            // (k - k0) * NP would become a 64-bit multiply-add on the vector unit)
+            reduce_entry(part, cur.band != 0, (int)cur.row, slot10, slot4, lane, p10);
         }
     };
 
@@ -999,7 +1127,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                 band = band && on;
                 float part[NP];
                 grad_pixel<false>(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, any_band, kl * NP, slot10, slot4, lane, p10);
+                reduce_entry(part, any_band, kl * (int)(NP * sizeof(float)), slot10, slot4, lane, p10);
             }
         }
         __syncthreads();
@@ -1026,7 +1154,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     }
     // The per-item loss (canvas.rs:45-58) from the forward kernel's per-block
     // sums, by the scene's first block, in a fixed order.
-    if (MODE == MODE_LOSS && !a.deterministic && blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+    if (MODE == MODE_LOSS && !a.deterministic && tg.bx == 0 && tg.by == 0 && wave == 0) {
         const int nblk = gridDim.x * gridDim.y;
         const double* pl = a.partial_loss + (size_t)b * nblk;
         double l = 0.0;
@@ -1229,12 +1357,15 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
 }
 
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
-                        float* rec, float* zero_grads, hipStream_t s, const float* bg_src, float* bg_dst) {
-    const int n = B * T, n_bg = bg_dst ? 3 * B : 0;
-    const int threads = n > n_bg ? n : n_bg;
-    if (threads == 0) return hipSuccess;
-    hipLaunchKernelGGL(setup_records, dim3((threads + 63) / 64), dim3(64), 0, s, params, n, W, H, sigma,
-                       setup_mode, rec, zero_grads, bg_src, bg_dst, n_bg);
+                        float* rec, float* zero_grads, hipStream_t s, const float* bg_src, float* bg_dst,
+                        const OrderArgs& o) {
+    if (B == 0 || (T == 0 && !bg_dst && !o.perm)) return hipSuccess;
+    if (o.perm && (o.gy + 1) * (o.gx + 1) > ORD_MAX_CELLS) return hipErrorInvalidValue;
+    // without an order, small workgroups spread the triangles over more CUs
+    const int n = o.perm ? SETUP_THREADS : 64;
+    const int gx = T > 0 ? (T + n - 1) / n : 1;
+    hipLaunchKernelGGL(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
+                       zero_grads, bg_src, bg_dst, o);
     return hipGetLastError();
 }
 

@@ -59,6 +59,7 @@ enum Kind : uint64_t {
     K_TILE_N,
     K_SRGB_F32,
     K_SRGB_U8,
+    K_ORDER,
 };
 
 // Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
@@ -86,6 +87,7 @@ struct TimedLaunch {
 
 struct drh_ctx {
     int device = 0;
+    int cus = 0;  // compute units of the device
     bool discrete = true;
     std::string info;
     std::mutex mu;
@@ -149,6 +151,7 @@ class Lease {
             std::lock_guard<std::mutex> g(ctx->mu);
             ctx->misses += 1;
         }
+        fresh_ = true;
         hipError_t e = hipMalloc(&buf_.ptr, bytes);
         if (e != hipSuccess) {
             buf_.ptr = nullptr;
@@ -165,6 +168,8 @@ class Lease {
     T* get() const {
         return static_cast<T*>(buf_.ptr);
     }
+    // The buffer was allocated by this lease (its contents are undefined).
+    bool fresh() const { return fresh_; }
 
     void release() {
         if (!buf_.ptr) return;
@@ -198,6 +203,7 @@ class Lease {
     }
 
   private:
+    bool fresh_ = false;
     drh_ctx* ctx_ = nullptr;
     uint64_t kind_ = 0;
     hipStream_t stream_ = nullptr;
@@ -386,6 +392,21 @@ int tile_entries(size_t ntiles, int T) {
     return (int)cap;
 }
 
+// The raster kernels' block order (OrderArgs) is made for a batch (B > 1)
+// whose grid has more blocks than the device has CUs (with fewer, every block
+// has a CU to itself) and whose scenes' difference grids fit in LDS. A single
+// scene is left in launch order: one workgroup would make its whole order,
+// which costs about what it saves on one scene's kernels. The forward kernel follows it when
+// its lists are short (T <= FWD_ORDER_MAX_T), so that the overlap count sets its
+// cost; with longer lists every block spends about the same building them, and
+// the order only costs it locality. The backward kernel always follows it.
+constexpr int FWD_ORDER_MAX_T = 256;
+
+bool use_order(const drh_ctx* ctx, int B, int gx, int gy) {
+    return B > 1 && (size_t)B * gx * gy > (size_t)ctx->cus &&
+           (size_t)(gx + 1) * (gy + 1) <= (size_t)drh::ORD_MAX_CELLS;
+}
+
 // The shared raster sequence: records, the forward pass, and (for the
 // gradient modes) the backward pass and the partial-row reduction.
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
@@ -396,7 +417,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     dim3 grid = drh::raster_grid(B, W, H);
     int nblk = (int)(grid.x * grid.y);
     size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pstate, tent, tn;
+    Lease rec, partials, ploss, pstate, tent, tn, order;
     const int cap2 = tile_entries(ntiles, T);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
@@ -408,11 +429,17 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * cap2 * sizeof(drh::TileEnt), s))) return rc;
         if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
     }
+    drh::OrderArgs ord{};
+    if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
+        if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
+        ord = {order.get<int>(), (int)grid.x, (int)grid.y};
+    }
     {
         KernelTimer kt(ctx, TK_SETUP, s);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
                                   mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, rec.get<float>(),
-                                  mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s),
+                                  mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s, nullptr, nullptr,
+                                  ord),
                 "setup_records launch");
     }
     drh::RasterArgs a{};
@@ -436,6 +463,8 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.losses = out_losses;
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
+    a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
+    a.perm_bwd = ord.perm;
     {
         KernelTimer kt(ctx, TK_RASTER, s);
         HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
@@ -456,10 +485,11 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
 
 // The forward record that drh_render_record leaves for drh_backward_recorded,
 // in device memory the caller owns: the triangle records, a copy of the
-// backgrounds, the per-pixel hand-over and the per-tile entries (with their
-// counts), each starting at a 256-byte boundary.
+// backgrounds, the per-pixel hand-over, the per-tile entries (with their
+// counts) and the backward kernel's block order, each starting at a 256-byte
+// boundary.
 struct RecordLayout {
-    size_t rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, total = 0;
+    size_t rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, ord = 0, total = 0;
     int cap2 = 0;
 };
 
@@ -481,6 +511,8 @@ RecordLayout record_layout(int64_t B, int64_t T, int64_t H, int64_t W) {
     off = up(off + ntiles * 2 * sizeof(int));
     L.tl_ent = off;
     off = up(off + ntiles * (size_t)L.cap2 * sizeof(drh::TileEnt));
+    L.ord = off;
+    off = up(off + ntiles / drh::WAVES * sizeof(int));
     L.total = off;
     return L;
 }
@@ -576,6 +608,7 @@ int drh_create(drh_ctx** out) {
     auto* c = new drh_ctx();
     c->device = dev;
     c->discrete = prop.integrated == 0;
+    c->cus = prop.multiProcessorCount;
     char buf[512];
     std::snprintf(buf, sizeof buf, "%s (%s, %d CUs, HIP)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
     c->info = buf;
@@ -775,10 +808,14 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     a.cap2 = L.cap2;
     a.tl_n = reinterpret_cast<int*>(base + L.tl_n);
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
+    const dim3 grid = drh::raster_grid(a.B, a.W, a.H);
+    drh::OrderArgs ord{};
+    if (use_order(ctx, a.B, (int)grid.x, (int)grid.y)) ord = {reinterpret_cast<int*>(base + L.ord), (int)grid.x, (int)grid.y};
+    a.perm_fwd = a.T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     {
         KernelTimer kt(ctx, TK_SETUP, s);
         HIP_TRY(drh::launch_setup(p.dev, a.B, a.T, a.W, a.H, sigma, drh::SETUP_RECORD, const_cast<float*>(a.rec),
-                                  nullptr, s, bg.dev, const_cast<float*>(a.bg)),
+                                  nullptr, s, bg.dev, const_cast<float*>(a.bg), ord),
                 "setup_records launch");
     }
     {
@@ -826,6 +863,8 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     a.tl_ent = reinterpret_cast<drh::TileEnt*>(const_cast<char*>(base + L.tl_ent));
     a.cap2 = L.cap2;
     a.tl_n = reinterpret_cast<int*>(const_cast<char*>(base + L.tl_n));
+    // the block order the record's setup made (use_order decides alike)
+    if (use_order(ctx, a.B, (int)grid.x, (int)grid.y)) a.perm_bwd = reinterpret_cast<const int*>(base + L.ord);
     a.grads = grads.dev;
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
