@@ -599,21 +599,48 @@ enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 // at the corners), the distance to segment j is sqrt(l^2 + ex^2) with
 // ex = max(0, -s, s - |e|). An edge whose lower bound exceeds the smallest
 // upper bound by more than the margin is never nearest.
+//
+// Two passes: the box test over the chunk compacts the candidates (in order)
+// into `list`, then the classification runs over the candidates only, 64 at a
+// time, and compacts the entries over them in place. Every branch of the
+// classification is taken by some lane of almost any 64 triangles, so the
+// wave's cost is per pass of 64, and the candidates are usually one pass.
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
                                  uint32_t* list, int lane, int live) {
-    int count = 0;
+    int nc = 0;
     for (int base = k0; base < k1; base += 64) {
-        int k = base + lane;
-        uint32_t cls = 0, plan = PLAN_GENERAL, extra = 0;
+        const int k = base + lane;
+        bool cand = false, in_box = false;
         if (k < k1) {
-            const float* r = rec + (size_t)k * REC;
-            const int* ri = reinterpret_cast<const int*>(r);
-            int flags = ri[R_FLAGS];
-            int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
-            if ((flags & live) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1) {
+            const int* ri = reinterpret_cast<const int*>(rec + (size_t)k * REC);
+            const int flags = ri[R_FLAGS];
+            const int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
+            cand = (flags & live) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1;
+            in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
+        }
+        const uint64_t mask = __ballot(cand);
+        if (cand) {
+            const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+            list[pos] = ((uint32_t)(k - k0) << 1) | (in_box ? 1u : 0u);
+        }
+        nc += (int)__popcll(mask);
+    }
+    // Entry i is written at count + rank <= i, a slot this or an earlier pass
+    // has read: the wave's LDS accesses complete in program order.
+    int count = 0;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        uint32_t cls = 0, plan = PLAN_GENERAL, extra = 0;
+        uint32_t kl = 0;
+        if (c0 + lane < nc) {
+            const uint32_t cd = list[c0 + lane];
+            kl = cd >> 1;
+            const float* r = rec + (size_t)(k0 + (int)kl) * REC;
+            const int flags = reinterpret_cast<const int*>(r)[R_FLAGS];
+            {
                 cls = CLS_PARTIAL;
-                const bool in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
+                const bool in_box = cd & 1u;
                 if (in_box) extra |= ENT_INBOX;
                 if (flags & F_FAST) {
                     float far = r[R_FAR], deep = r[R_DEEP];
@@ -684,11 +711,11 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                 }
             }
         }
-        uint64_t mask = __ballot(cls != 0);
+        const uint64_t mask = __ballot(cls != 0);
         if (cls != 0) {
-            int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = ((uint32_t)(k - k0) << 8) | extra | (plan << 2) | cls;
+            const int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+            list[pos] = (kl << 8) | extra | (plan << 2) | cls;
         }
         count += (int)__popcll(mask);
     }
@@ -868,7 +895,18 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                     const float o = r.f(R_C + ch) * w + col[ch] * omw;
                     col[ch] = on ? o : col[ch];
                 }
-                if (MODE != MODE_RENDER) trans_mul(tot, taped ? omw : 1.0f);
+                if (MODE != MODE_RENDER) {
+                    // trans_mul, by a plain product while it needs neither a zero
+                    // count nor a rescaling: a factor (in [0, 1], raster.rs:48)
+                    // that is zero, or a product below 2^-64 (or NaN), fails the
+                    // test, and only then does the wave take the counting step.
+                    const float f = taped ? omw : 1.0f;
+                    const float qn = tot.q * f;
+                    if (__ballot(!(qn >= 5.421010862427522e-20f)) == 0)
+                        tot.q = qn;
+                    else
+                        trans_mul(tot, f);
+                }
             }
             if (MODE != MODE_RENDER) {
                 uint64_t onm = __ballot(taped);
