@@ -742,6 +742,18 @@ __device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, u
         act = act && (unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX)) &&
               (unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1));
     band = act;
+    if (FAST && (r.i(R_FLAGS) & F_FAST) && ((ent >> 2) & 3u) != PLAN_GENERAL) {
+        // A single-edge plan holds for every pixel of the tile, so every lane
+        // evaluates its edge: no classification and no divergent branch. A deep
+        // pixel (more than 17 sigma + slack inside every edge line) gets
+        // exp(-x) < 2^-24 and coverage exactly 1.0f, as classified; a far one
+        // (beyond `far`) a weight below MIN_WEIGHT, skipped as classified.
+        g = geometry1(r, rp, p, (ent >> 2) & 7u);
+        cov = sigmoid_f<true>(g.sd * rsig);
+        w = alpha * cov;
+        band = act && cov != 1.0f;
+        return act && !(w <= MIN_WEIGHT);
+    }
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
         // Conservative classification by the outward edge-line distances.
         float l0 = fmaf(p.px, r.f(R_N + 0), fmaf(p.py, r.f(R_N + 1), -r.f(R_OFF + 0)));
@@ -753,6 +765,10 @@ __device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, u
     }
     if (band) exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
+    // `band` hands the backward pass the lanes whose coverage it must evaluate:
+    // where the exact coverage is 1.0f it takes 1.0f without evaluating, and
+    // the vertex terms, proportional to cov (1 - cov), are zero.
+    band = band && cov != 1.0f;
     return act && !(w <= MIN_WEIGHT);
 }
 
