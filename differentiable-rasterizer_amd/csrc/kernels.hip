@@ -729,20 +729,25 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
 // branch, so the wave runs it once for the lanes that need it.
 template <bool FAST>
 __device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, uint32_t ent, int x, int y, Pix p,
-                                   bool valid, float& w, float& cov, bool& band, Geo& g, float rsig, float sig) {
+                                   uint64_t validm, float& w, float& cov, bool& band, Geo& g, float rsig, float sig) {
     const float alpha = r.f(R_A);
     cov = 1.0f;
+    // The lanes in play as a wave mask (`validm`: the lanes whose pixel is in
+    // the image), narrowed by the box test unless the tile lies inside the box:
+    // the tests stay scalar mask operations instead of per-lane 0/1 values.
+    uint64_t actm = validm;
     if ((ent & 3u) == CLS_FULL) {
         band = false;
         w = alpha;
-        return valid && !(w <= MIN_WEIGHT);
+        return __builtin_amdgcn_inverse_ballot_w64(actm) && !(w <= MIN_WEIGHT);
     }
-    bool act = valid;
     if (!(ent & ENT_INBOX))
-        act = act && (unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX)) &&
-              (unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1));
+        actm &= __builtin_amdgcn_ballot_w64((unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX))) &
+                __builtin_amdgcn_ballot_w64((unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1)));
+    bool act = __builtin_amdgcn_inverse_ballot_w64(actm);
     band = act;
-    if (FAST && (r.i(R_FLAGS) & F_FAST) && ((ent >> 2) & 3u) != PLAN_GENERAL) {
+    // build_list gives a single-edge plan to fast-path triangles (F_FAST) only
+    if (FAST && ((ent >> 2) & 3u) != PLAN_GENERAL) {
         // A single-edge plan holds for every pixel of the tile, so every lane
         // evaluates its edge: no classification and no divergent branch. A deep
         // pixel (more than 17 sigma + slack inside every edge line) gets
@@ -867,6 +872,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     __shared__ double loss[WAVES];
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
+    const uint64_t validm = __ballot(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -900,7 +906,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             float w = 0.0f, cov;
             bool band;
             Geo g;
-            bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+            bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, band, g, rsig, sig);
             // MODE_RECORD draws what a render draws but hands over what the
             // taped forward keeps (F_TAPE); in the other modes the two agree.
             const bool taped = on && (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE));
@@ -1088,6 +1094,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     __shared__ float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
+    const uint64_t validm = __ballot(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -1175,7 +1182,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                 float w = 0.0f, cov = 0.0f;
                 bool band = false;
                 Geo g;
-                bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, tg.valid, w, cov, band, g, rsig, sig);
+                bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, band, g, rsig, sig);
                 if (__ballot(on) == 0) continue;
                 const bool any_band = __ballot(on && band) != 0;
                 band = band && on;
