@@ -566,6 +566,11 @@ __device__ inline float wave_reduce4(float a0, float a1, float a2, float a3) {
     return c;
 }
 
+// The wave's lanes for which `c` holds (inactive lanes 0). HIP's __ballot widens
+// the condition to an integer and compares it again, two vector instructions
+// more per call than the builtin, which takes the compare's lane mask as is.
+__device__ inline uint64_t lane_mask(bool c) { return __builtin_amdgcn_ballot_w64(c); }
+
 // Wave-uniform copies of values every lane holds (loaded from one address).
 // The builtin returns int: widen through uint32_t, never by sign extension.
 __device__ inline uint32_t uniform_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
@@ -619,7 +624,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
             cand = (flags & live) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1;
             in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
         }
-        const uint64_t mask = __ballot(cand);
+        const uint64_t mask = lane_mask(cand);
         if (cand) {
             const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
@@ -711,7 +716,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                 }
             }
         }
-        const uint64_t mask = __ballot(cls != 0);
+        const uint64_t mask = lane_mask(cls != 0);
         if (cls != 0) {
             const int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
@@ -722,30 +727,31 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
     return count;
 }
 
-// Per-pixel weight of one triangle: returns false when the pair is skipped
-// (outside the box, classified far outside, or w <= MIN_WEIGHT). `band` tells
-// whether the exact path ran, and then `g` holds its geometry. The tests are
+// Per-pixel weight of one triangle: returns the mask of the lanes where the
+// pair contributes (not outside the box, not classified far outside, and
+// w > MIN_WEIGHT). `bandm` holds the lanes where the exact path ran with a
+// coverage below 1.0f, and there `g` holds its geometry. The tests are
 // predicates rather than branches; only the exact path is a (divergent)
 // branch, so the wave runs it once for the lanes that need it.
 template <bool FAST>
-__device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, uint32_t ent, int x, int y, Pix p,
-                                   uint64_t validm, float& w, float& cov, bool& band, Geo& g, float rsig, float sig) {
+__device__ inline uint64_t pair_weight(const Rec& r, const float* __restrict__ rp, uint32_t ent, int x, int y,
+                                       Pix p, uint64_t validm, float& w, float& cov, uint64_t& bandm, Geo& g,
+                                       float rsig, float sig) {
     const float alpha = r.f(R_A);
     cov = 1.0f;
-    // The lanes in play as a wave mask (`validm`: the lanes whose pixel is in
-    // the image), narrowed by the box test unless the tile lies inside the box:
-    // the tests stay scalar mask operations instead of per-lane 0/1 values.
+    // The lane sets are wave masks (`validm`: the lanes whose pixel is in the
+    // image), each test one compare's mask ANDed in: kept as scalar mask
+    // operations instead of per-lane 0/1 values, which the compiler widens a
+    // combined condition into before taking its mask.
     uint64_t actm = validm;
     if ((ent & 3u) == CLS_FULL) {
-        band = false;
+        bandm = 0;
         w = alpha;
-        return __builtin_amdgcn_inverse_ballot_w64(actm) && !(w <= MIN_WEIGHT);
+        return actm & lane_mask(!(w <= MIN_WEIGHT));
     }
     if (!(ent & ENT_INBOX))
-        actm &= __builtin_amdgcn_ballot_w64((unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX))) &
-                __builtin_amdgcn_ballot_w64((unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1)));
-    bool act = __builtin_amdgcn_inverse_ballot_w64(actm);
-    band = act;
+        actm &= lane_mask((unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX))) &
+                lane_mask((unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1)));
     // build_list gives a single-edge plan to fast-path triangles (F_FAST) only
     if (FAST && ((ent >> 2) & 3u) != PLAN_GENERAL) {
         // A single-edge plan holds for every pixel of the tile, so every lane
@@ -756,25 +762,26 @@ __device__ inline bool pair_weight(const Rec& r, const float* __restrict__ rp, u
         g = geometry1(r, rp, p, (ent >> 2) & 7u);
         cov = sigmoid_f<true>(g.sd * rsig);
         w = alpha * cov;
-        band = act && cov != 1.0f;
-        return act && !(w <= MIN_WEIGHT);
+        bandm = actm & lane_mask(cov != 1.0f);
+        return actm & lane_mask(!(w <= MIN_WEIGHT));
     }
+    bandm = actm;
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
         // Conservative classification by the outward edge-line distances.
         float l0 = fmaf(p.px, r.f(R_N + 0), fmaf(p.py, r.f(R_N + 1), -r.f(R_OFF + 0)));
         float l1 = fmaf(p.px, r.f(R_N + 2), fmaf(p.py, r.f(R_N + 3), -r.f(R_OFF + 1)));
         float l2 = fmaf(p.px, r.f(R_N + 4), fmaf(p.py, r.f(R_N + 5), -r.f(R_OFF + 2)));
         float lm = fmaxf(fmaxf(l0, l1), l2);
-        act = act && !(lm > r.f(R_FAR));
-        band = act && !(lm < r.f(R_DEEP));
+        actm &= lane_mask(!(lm > r.f(R_FAR)));
+        bandm = actm & lane_mask(!(lm < r.f(R_DEEP)));
     }
-    if (band) exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
+    if (__builtin_amdgcn_inverse_ballot_w64(bandm)) exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
-    // `band` hands the backward pass the lanes whose coverage it must evaluate:
+    // `bandm` hands the backward pass the lanes whose coverage it must evaluate:
     // where the exact coverage is 1.0f it takes 1.0f without evaluating, and
     // the vertex terms, proportional to cov (1 - cov), are zero.
-    band = band && cov != 1.0f;
-    return act && !(w <= MIN_WEIGHT);
+    bandm &= lane_mask(cov != 1.0f);
+    return actm & lane_mask(!(w <= MIN_WEIGHT));
 }
 
 struct Trans {
@@ -872,7 +879,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     __shared__ double loss[WAVES];
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
-    const uint64_t validm = __ballot(tg.valid);  // lanes whose pixel is in the image
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -904,12 +911,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
             float w = 0.0f, cov;
-            bool band;
+            uint64_t bandm;
             Geo g;
-            bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, band, g, rsig, sig);
+            const uint64_t onm = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+            const bool on = __builtin_amdgcn_inverse_ballot_w64(onm);
             // MODE_RECORD draws what a render draws but hands over what the
             // taped forward keeps (F_TAPE); in the other modes the two agree.
-            const bool taped = on && (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE));
+            const uint64_t tapedm = (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE)) ? onm : 0;
+            const bool taped = __builtin_amdgcn_inverse_ballot_w64(tapedm);
             {
                 // raster.rs:60-66, kept only where the pair contributes
                 const float omw = 1.0f - w;
@@ -924,22 +933,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                     // test, and only then does the wave take the counting step.
                     const float f = taped ? omw : 1.0f;
                     const float qn = tot.q * f;
-                    if (__ballot(!(qn >= 5.421010862427522e-20f)) == 0)
+                    if (lane_mask(!(qn >= 5.421010862427522e-20f)) == 0)
                         tot.q = qn;
                     else
                         trans_mul(tot, f);
                 }
             }
             if (MODE != MODE_RENDER) {
-                uint64_t onm = __ballot(taped);
-                if (onm != 0) {
-                    const uint64_t bm = __ballot(taped && band);
+                if (tapedm != 0) {
                     if (n2 < cap2 && lane == 0) {
                         TileEnt e;
                         e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
                         e.row = (ent >> 8) * (uint32_t)(NP * sizeof(float));
-                        e.on = onm;
-                        e.band = bm;
+                        e.on = tapedm;
+                        e.band = tapedm & bandm;
                         te[n2] = e;
                     }
                     n2++;
@@ -1094,7 +1101,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     __shared__ float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
-    const uint64_t validm = __ballot(tg.valid);  // lanes whose pixel is in the image
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
@@ -1126,7 +1133,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     lds_float* const slot10 = (lds_float*)accw + (p10 >= 0 ? p10 : 0);
     lds_float* const slot4 = (lds_float*)accw + 6 + (lane >> 4);
     int i2 = 0;
-    const bool plain = __ballot(st.tot.z != 0 || st.tot.e != 0) == 0;
+    const bool plain = lane_mask(st.tot.z != 0 || st.tot.e != 0) == 0;
 
     // The entries the forward kernel recorded: which lanes contribute and
     // which of them took the exact path are known; only w is recomputed. The
@@ -1180,12 +1187,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                 const float* rp = rec + (size_t)(k0 + kl) * REC;
                 const Rec r = load_rec(rp);
                 float w = 0.0f, cov = 0.0f;
-                bool band = false;
+                uint64_t bandm;
                 Geo g;
-                bool on = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, band, g, rsig, sig);
-                if (__ballot(on) == 0) continue;
-                const bool any_band = __ballot(on && band) != 0;
-                band = band && on;
+                const uint64_t onm = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+                if (onm == 0) continue;
+                bandm &= onm;
+                const bool any_band = bandm != 0;
+                const bool on = __builtin_amdgcn_inverse_ballot_w64(onm);
+                const bool band = __builtin_amdgcn_inverse_ballot_w64(bandm);
                 float part[NP];
                 grad_pixel<false>(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
                 reduce_entry(part, any_band, kl * (int)(NP * sizeof(float)), slot10, slot4, lane, p10);
