@@ -616,15 +616,16 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
     int nc = 0;
     for (int base = k0; base < k1; base += 64) {
         const int k = base + lane;
-        bool cand = false, in_box = false;
-        if (k < k1) {
-            const int* ri = reinterpret_cast<const int*>(rec + (size_t)k * REC);
-            const int flags = ri[R_FLAGS];
-            const int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
-            cand = (flags & live) && tx0 < bx1 && bx0 < tx1 && ty0 < by1 && by0 < ty1;
-            in_box = bx0 <= tx0 && tx1 <= bx1 && by0 <= ty0 && ty1 <= by1;
-        }
-        const uint64_t mask = lane_mask(cand);
+        // Lanes past the chunk read its last record (in bounds) and are masked
+        // out; the tests are single-compare lane masks, ANDed as scalars.
+        const int* ri = reinterpret_cast<const int*>(rec + (size_t)min(k, k1 - 1) * REC);
+        const int flags = ri[R_FLAGS];
+        const int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
+        const uint64_t mask = lane_mask(k < k1) & lane_mask((flags & live) != 0) & lane_mask(tx0 < bx1) &
+                              lane_mask(bx0 < tx1) & lane_mask(ty0 < by1) & lane_mask(by0 < ty1);
+        const bool cand = __builtin_amdgcn_inverse_ballot_w64(mask);
+        const bool in_box = __builtin_amdgcn_inverse_ballot_w64(lane_mask(bx0 <= tx0) & lane_mask(tx1 <= bx1) &
+                                                                lane_mask(by0 <= ty0) & lane_mask(ty1 <= by1));
         if (cand) {
             const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
