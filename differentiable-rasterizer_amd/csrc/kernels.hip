@@ -921,10 +921,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             const uint64_t tapedm = (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE)) ? onm : 0;
             const bool taped = __builtin_amdgcn_inverse_ballot_w64(tapedm);
             {
-                // raster.rs:60-66, kept only where the pair contributes
+                // raster.rs:60-66, kept only where the pair contributes, as
+                // col + w (c - col): one rounding fewer than c w + col (1 - w),
+                // and the form the backward kernel rebuilds the colour with
                 const float omw = 1.0f - w;
                 for (int ch = 0; ch < 3; ch++) {
-                    const float o = r.f(R_C + ch) * w + col[ch] * omw;
+                    const float o = fmaf(w, r.f(R_C + ch) - col[ch], col[ch]);
                     col[ch] = on ? o : col[ch];
                 }
                 if (MODE != MODE_RENDER) {
