@@ -768,15 +768,15 @@ __device__ inline uint64_t pair_weight(const Rec& r, const float* __restrict__ r
     }
     bandm = actm;
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
-        // Conservative classification by the outward edge-line distances.
-        float l0 = fmaf(p.px, r.f(R_N + 0), fmaf(p.py, r.f(R_N + 1), -r.f(R_OFF + 0)));
-        float l1 = fmaf(p.px, r.f(R_N + 2), fmaf(p.py, r.f(R_N + 3), -r.f(R_OFF + 1)));
-        float l2 = fmaf(p.px, r.f(R_N + 4), fmaf(p.py, r.f(R_N + 5), -r.f(R_OFF + 2)));
-        float lm = fmaxf(fmaxf(l0, l1), l2);
-        actm &= lane_mask(!(lm > r.f(R_FAR)));
-        bandm = actm & lane_mask(!(lm < r.f(R_DEEP)));
+        // The three-edge path at every lane, for the same reasons as a single
+        // edge: a pixel that the edge-line distances would class deep gets
+        // coverage exactly 1.0f, a far one a weight below MIN_WEIGHT.
+        asm volatile("");
+        g = geometry<true>(r, p);
+        cov = sigmoid_f<true>(g.sd * rsig);
+    } else if (__builtin_amdgcn_inverse_ballot_w64(bandm)) {
+        exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     }
-    if (__builtin_amdgcn_inverse_ballot_w64(bandm)) exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     w = alpha * cov;
     // `bandm` hands the backward pass the lanes whose coverage it must evaluate:
     // where the exact coverage is 1.0f it takes 1.0f without evaluating, and
