@@ -10,6 +10,7 @@ constexpr int NP = 10;    // parameters per triangle (scene.rs:21)
 constexpr int TILE = 8;   // a wave covers an 8x8 pixel tile, one pixel per lane
 constexpr int WAVES = 4;  // waves per block: 2x2 tiles, a 16x16 pixel region
 constexpr int CH = 128;   // triangles per chunk (LDS accumulators are per chunk)
+static_assert((CH * NP) % 4 == 0, "accumulator rows are cleared and summed four floats at a time");
 
 // Per-triangle record, REC floats, written by setup_records. The hot loops
 // load fields [0, REC_HOT) of one record per list entry; the rest is read

@@ -1101,7 +1101,7 @@ template <int MODE, bool FAST, bool REBUILD>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? 6 : 7))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
                                                                const TileEnt* __restrict__ ents) {
     __shared__ uint32_t list[WAVES][CH];
-    __shared__ float acc[WAVES][CH * NP];
+    __shared__ __attribute__((aligned(16))) float acc[WAVES][CH * NP];
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
@@ -1168,7 +1168,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
         int nk = k1 - k0;
-        for (int j = lane; j < nk * NP; j += 64) accw[j] = 0.0f;
+        {
+            // the wave's whole accumulator row (CH * NP floats, 16-byte aligned),
+            // four floats per store
+            float4* acc4 = reinterpret_cast<float4*>(accw);
+            for (int j = lane; j < CH * NP / 4; j += 64) acc4[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
