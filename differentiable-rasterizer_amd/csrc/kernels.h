@@ -103,6 +103,18 @@ struct RasterArgs {
     int chw;               // images, targets and grad_in are B x 3 x H x W (else B x H x W x 3)
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
     const int* perm_bwd;   // block order of the backward kernel or null
+    const int* halt;       // null, or a flag: every block returns at entry once it is >= 0
+};
+
+// Head of a forward record (drh_render_record), written by setup_records:
+// what a later backward of the record must agree with.
+constexpr uint32_t RECORD_MAGIC = 0x44524831u;  // "DRH1"
+struct RecordHead {
+    uint32_t magic;
+    uint32_t exact;  // the forward ran with IEEE geometry (DRH_EXACT_MATH)
+    float sigma;
+    int32_t B, T, H, W;
+    uint32_t pad;
 };
 
 // Device-side state of a running fit (fit.rs:197-211).
@@ -123,15 +135,19 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
 
 // bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src; with
 // o.cnt, the block order is made (OrderArgs).
+// halt (optional): the kernel does nothing once *halt >= 0 (a stopped fit).
+// head (optional): receives head_val (a forward record's head).
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
                         float* rec, float* zero_grads, hipStream_t s, const float* bg_src = nullptr,
-                        float* bg_dst = nullptr, const OrderArgs& o = OrderArgs{});
+                        float* bg_dst = nullptr, const OrderArgs& o = OrderArgs{}, const int* halt = nullptr,
+                        RecordHead* head = nullptr, const RecordHead& head_val = RecordHead{});
 // n floats set to zero by a kernel (no memset node, so callers may capture it).
 hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s);
+// npix3: 3 H W, the divisor of the per-item loss (canvas.rs:45-58)
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
-                         int npix3, float* grads, float* losses, hipStream_t s);
+                         double npix3, float* grads, float* losses, hipStream_t s, const int* halt = nullptr);
 // 256 floats passed by value to the sRGB kernels: the byte thresholds of the
 // encoding (entry k the smallest linear value whose byte is k; entry 0 unused)
 // or the decoded value of each byte.

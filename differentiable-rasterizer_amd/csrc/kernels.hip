@@ -272,9 +272,13 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
                                                                int H, float sigma, int setup_mode,
                                                                float* __restrict__ rec, float* __restrict__ zero_grads,
                                                                const float* __restrict__ bg_src,
-                                                               float* __restrict__ bg_dst, OrderArgs o) {
+                                                               float* __restrict__ bg_dst, OrderArgs o,
+                                                               const int* __restrict__ halt,
+                                                               RecordHead* __restrict__ head, RecordHead head_val) {
     __shared__ int cells[ORD_MAX_CELLS];
+    if (halt && *halt >= 0) return;
     const int b = blockIdx.y, k = blockIdx.x * blockDim.x + threadIdx.x, pitch = o.gx + 1;
+    if (head && b == 0 && blockIdx.x == 0 && threadIdx.x == 0) *head = head_val;
     const bool order = o.perm && blockIdx.x == 0;
     // A record kept for a later backward holds its own copy of the backgrounds.
     if (bg_dst && blockIdx.x == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
@@ -878,6 +882,7 @@ template <int MODE, bool FAST>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8))) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ double loss[WAVES];
+    if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
@@ -1102,6 +1107,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                                                                const TileEnt* __restrict__ ents) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ __attribute__((aligned(16))) float acc[WAVES][CH * NP];
+    if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
@@ -1248,10 +1254,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
 constexpr int RED_WAVES = 16;
 __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* __restrict__ partials,
                                                                   const double* __restrict__ partial_loss,
-                                                                  int nblk, int T, int npix3,
+                                                                  int nblk, int T, double npix3,
                                                                   float* __restrict__ grads,
-                                                                  float* __restrict__ losses) {
+                                                                  float* __restrict__ losses,
+                                                                  const int* __restrict__ halt) {
     __shared__ float part[RED_WAVES][64];
+    if (halt && *halt >= 0) return;
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = T * NP;
@@ -1279,7 +1287,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* _
         double s = 0.0;
         for (int rr = lane; rr < nblk; rr += 64) s += partial_loss[(size_t)b * nblk + rr];
         s = wave_sum_f64(s);
-        if (lane == 0) losses[b] = (float)(s / (double)npix3);
+        if (lane == 0) losses[b] = (float)(s / npix3);
     }
 }
 
@@ -1436,14 +1444,14 @@ hipError_t launch_fit_tail(int iter, const float* loss, float* params, const flo
 
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
                         float* rec, float* zero_grads, hipStream_t s, const float* bg_src, float* bg_dst,
-                        const OrderArgs& o) {
-    if (B == 0 || (T == 0 && !bg_dst && !o.perm)) return hipSuccess;
+                        const OrderArgs& o, const int* halt, RecordHead* head, const RecordHead& head_val) {
+    if (B == 0 || (T == 0 && !bg_dst && !o.perm && !head)) return hipSuccess;
     if (o.perm && (o.gy + 1) * (o.gx + 1) > ORD_MAX_CELLS) return hipErrorInvalidValue;
     // without an order, small workgroups spread the triangles over more CUs
     const int n = o.perm ? SETUP_THREADS : 64;
     const int gx = T > 0 ? (T + n - 1) / n : 1;
     hipLaunchKernelGGL(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
-                       zero_grads, bg_src, bg_dst, o);
+                       zero_grads, bg_src, bg_dst, o, halt, head, head_val);
     return hipGetLastError();
 }
 
@@ -1493,11 +1501,11 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
 }
 
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
-                         int npix3, float* grads, float* losses, hipStream_t s) {
+                         double npix3, float* grads, float* losses, hipStream_t s, const int* halt) {
     int cols = T * NP;
     dim3 grid((cols + 63) / 64 > 0 ? (cols + 63) / 64 : 1, B);
     hipLaunchKernelGGL(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, T, npix3,
-                       grads, losses);
+                       grads, losses, halt);
     return hipGetLastError();
 }
 

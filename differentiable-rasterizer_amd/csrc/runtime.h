@@ -1,0 +1,222 @@
+// Internal declarations shared by the host sources behind the C ABI
+// (runtime.hip: context, pool, raster entry points; fit.hip: the fit loop and
+// the step-wise fitter; scratch.hip: the entry point that allocates nothing).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "diffrast_hip.h"
+#include "kernels.h"
+
+namespace drh_rt {
+
+// Sets the calling thread's drh_last_error() message and returns `code`.
+int fail(int code, const std::string& msg);
+const char* last_error_text();
+int hip_fail(hipError_t e, const char* what);
+
+#define HIP_TRY(expr, what)                                       \
+    do {                                                          \
+        hipError_t _e = (expr);                                   \
+        if (_e != hipSuccess) return ::drh_rt::hip_fail(_e, what); \
+    } while (0)
+
+// What a pooled buffer holds; part of the pool key so that, as in the
+// reference pool (crates/diffrast-gpu/src/lib.rs:132-143), a buffer is only
+// reused for the same purpose at exactly the same size.
+enum Kind : uint64_t {
+    K_REC = 1,
+    K_PARTIALS,
+    K_PLOSS,
+    K_IN_PARAMS,
+    K_IN_BG,
+    K_IN_IMAGES,
+    K_OUT_IMAGES,
+    K_OUT_GRADS,
+    K_OUT_LOSSES,
+    K_FIT_F32,
+    K_FIT_STATE,
+    K_PIXSTATE,
+    K_TILE_ENT,
+    K_TILE_N,
+    K_SRGB_F32,
+    K_SRGB_U8,
+    K_ORDER,
+    K_FIT_TARGET,
+};
+
+// Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
+// released beyond it are freed.
+constexpr uint64_t POOL_BYTE_LIMIT = 512ull << 20;
+
+struct PoolBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t ev = nullptr;       // recorded when the last user released it (multi-stream)
+    hipStream_t stream = nullptr;  // stream of that last use
+    bool used = false;
+    bool ev_recorded = false;      // `ev` marks the end of the last use
+};
+
+enum TimedKernel : int { TK_SETUP = 0, TK_RASTER, TK_REDUCE, TK_ADAM, TK_BACKWARD, TK_COUNT };
+struct TimedLaunch {
+    int kernel;
+    hipEvent_t start, stop;
+};
+
+}  // namespace drh_rt
+
+struct drh_ctx {
+    int device = 0;
+    int cus = 0;  // compute units of the device
+    bool discrete = true;
+    std::string info;
+    std::mutex mu;
+    std::unordered_map<uint64_t, std::vector<drh_rt::PoolBuf>> free_bufs;
+    uint64_t hits = 0, misses = 0, bytes = 0;
+    // Set once buffers have been used on more than one stream. Until then
+    // every use of a buffer is ordered by the one stream and releases record
+    // no event (an event record costs a GPU-side marker per buffer per call).
+    bool multi_stream = false;
+    // kernel timing (drh_timing_enable / drh_timing_read)
+    bool timing = false;
+    std::vector<drh_rt::TimedLaunch> pending;
+    // Heads of the forward records this context made (record address -> head),
+    // so that drh_backward_recorded checks its arguments without reading the
+    // device; a record made elsewhere has its head read from the device.
+    std::unordered_map<const void*, drh::RecordHead> records;
+};
+
+namespace drh_rt {
+
+inline uint64_t pool_key(uint64_t kind, size_t bytes) { return (kind << 56) | (uint64_t)bytes; }
+
+// A buffer borrowed from the pool for the duration of one call (or of a
+// fitter's life). Reuse on the stream of the last use is ordered by that
+// stream. Once a context sees a second stream, releases record an event that a
+// user on another stream waits for; at that first switch the device is
+// synchronized once, since the earlier uses recorded none. Either way reuse
+// never races queued work.
+class Lease {
+  public:
+    Lease() = default;
+    Lease(const Lease&) = delete;
+    Lease& operator=(const Lease&) = delete;
+    ~Lease() { release(); }
+
+    int acquire(drh_ctx* ctx, uint64_t kind, size_t bytes, hipStream_t s);
+    template <class T>
+    T* get() const {
+        return static_cast<T*>(buf_.ptr);
+    }
+    void release();
+
+  private:
+    drh_ctx* ctx_ = nullptr;
+    uint64_t kind_ = 0;
+    hipStream_t stream_ = nullptr;
+    PoolBuf buf_;
+};
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Host wait bounded like GpuRasterizer::POLL_TIMEOUT (crates/diffrast-gpu/src/lib.rs:229).
+int wait_stream(hipStream_t s);
+
+// Argument checks shared by the raster entry points, with the reference
+// binding's messages (crates/diffrast-py/src/lib.rs:162-195).
+int check_sizes(int64_t B, int64_t T, int64_t H, int64_t W);
+int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float sigma);
+
+// Device view of an input array: the pointer itself, or a pooled copy.
+struct Staged {
+    Lease lease;
+    const float* dev = nullptr;
+};
+int stage_in(drh_ctx* ctx, Staged& st, uint64_t kind, const float* src, size_t n, bool host, hipStream_t s);
+
+// Device output: the caller's pointer, or a pooled buffer copied back by copy_back.
+struct Out {
+    Lease lease;
+    float* dev = nullptr;
+    float* host_dst = nullptr;
+    size_t n = 0;
+};
+int stage_out(drh_ctx* ctx, Out& o, uint64_t kind, float* dst, size_t n, bool host, hipStream_t s);
+int copy_back(Out& o, hipStream_t s);
+
+// With host pointers or DRH_SYNC: waits for the stream.
+int finish(uint32_t flags, hipStream_t s);
+
+// f32::powi with a runtime exponent (square-and-multiply, as the
+// compiler-builtins __powisf2 that the reference's Adam calls).
+float powi_f32(float a, int32_t b);
+
+// Brackets one kernel launch with events when the context is timing.
+class KernelTimer {
+  public:
+    KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s, bool enabled = true);
+    ~KernelTimer();
+
+  private:
+    drh_ctx* ctx_;
+    hipStream_t s_;
+    TimedLaunch l_{};
+    bool on_ = false;
+};
+
+// Entries the forward kernel records per tile: all T while that fits `budget`
+// bytes, else as many as fit (at least `min_cap`); DRH_MAX_TILE_ENTRIES in the
+// environment lowers the cap, so tests can force the rebuild path.
+constexpr size_t TILE_ENT_BUDGET = 1ull << 30;
+int tile_entries(size_t ntiles, int T, size_t budget = TILE_ENT_BUDGET, size_t min_cap = drh::CAP2_MIN);
+
+// The forward kernel follows the block order when its lists are short.
+constexpr int FWD_ORDER_MAX_T = 256;
+bool use_order(const drh_ctx* ctx, int B, int gx, int gy);
+
+// Device buffers of one raster call besides its inputs and outputs.
+struct RasterBufs {
+    float* rec = nullptr;           // B*T*REC
+    float* partials = nullptr;      // B*nblk*T*NP (deterministic gradient modes)
+    double* ploss = nullptr;        // B*nblk (gradient modes)
+    drh::PixState* pstate = nullptr;  // B*H*W (gradient modes)
+    drh::TileEnt* tent = nullptr;   // ntiles*cap2 (gradient modes)
+    int* tn = nullptr;              // ntiles*2 (gradient modes)
+    int* order = nullptr;           // B*nblk, or null: launch order
+    int cap2 = 0;
+};
+
+// The shared raster sequence over given buffers: records, the forward pass,
+// and (gradient modes) the backward pass and the partial-row reduction. With
+// `halt`, every kernel does nothing once *halt >= 0.
+// `timed`: the launches take part in drh_timing_* (events are created for them).
+int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
+                    int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
+                    uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt = nullptr,
+                    bool timed = true);
+
+// run_raster_bufs over pooled buffers.
+int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
+               int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
+               hipStream_t s, const int* halt = nullptr);
+
+}  // namespace drh_rt

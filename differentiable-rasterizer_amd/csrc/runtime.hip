@@ -1,6 +1,7 @@
 // Host runtime behind the C ABI in include/diffrast_hip.h: argument checks,
 // the device-buffer pool, host/device pointer staging, kernel sequencing and
-// the device-side fit loop.
+// the raster, record, Adam and sRGB entry points. The fit loop is in fit.hip,
+// the entry point that allocates nothing in scratch.hip.
 
 #include <hip/hip_runtime.h>
 
@@ -15,14 +16,17 @@
 #include <unordered_map>
 #include <vector>
 
-#include "diffrast_hip.h"
-#include "kernels.h"
+#include "runtime.h"
 
 using drh::NP;
 
-namespace {
+namespace drh_rt {
 
+namespace {
 thread_local std::string g_err;
+}  // namespace
+
+const char* last_error_text() { return g_err.c_str(); }
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -33,198 +37,82 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(DRH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-#define HIP_TRY(expr, what)                       \
-    do {                                          \
-        hipError_t _e = (expr);                   \
-        if (_e != hipSuccess) return hip_fail(_e, what); \
-    } while (0)
-
-// What a pooled buffer holds; part of the pool key so that, as in the
-// reference pool (crates/diffrast-gpu/src/lib.rs:132-143), a buffer is only
-// reused for the same purpose at exactly the same size.
-enum Kind : uint64_t {
-    K_REC = 1,
-    K_PARTIALS,
-    K_PLOSS,
-    K_IN_PARAMS,
-    K_IN_BG,
-    K_IN_IMAGES,
-    K_OUT_IMAGES,
-    K_OUT_GRADS,
-    K_OUT_LOSSES,
-    K_FIT_F32,
-    K_FIT_STATE,
-    K_PIXSTATE,
-    K_TILE_ENT,
-    K_TILE_N,
-    K_SRGB_F32,
-    K_SRGB_U8,
-    K_ORDER,
-};
-
-// Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
-// released beyond it are freed.
-constexpr uint64_t POOL_BYTE_LIMIT = 512ull << 20;
-
-struct PoolBuf {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-    hipEvent_t ev = nullptr;          // recorded when the last user released it (multi-stream)
-    hipStream_t stream = nullptr;     // stream of that last use
-    bool used = false;
-    bool ev_recorded = false;         // `ev` marks the end of the last use
-};
-
-}  // namespace
-
-namespace {
-enum TimedKernel : int { TK_SETUP = 0, TK_RASTER, TK_REDUCE, TK_ADAM, TK_BACKWARD, TK_COUNT };
-struct TimedLaunch {
-    int kernel;
-    hipEvent_t start, stop;
-};
-}  // namespace
-
-struct drh_ctx {
-    int device = 0;
-    int cus = 0;  // compute units of the device
-    bool discrete = true;
-    std::string info;
-    std::mutex mu;
-    std::unordered_map<uint64_t, std::vector<PoolBuf>> free_bufs;
-    uint64_t hits = 0, misses = 0, bytes = 0;
-    // Set once buffers have been used on more than one stream. Until then
-    // every use of a buffer is ordered by the one stream and releases record
-    // no event (an event record costs a GPU-side marker per buffer per call).
-    bool multi_stream = false;
-    // kernel timing (drh_timing_enable / drh_timing_read)
-    bool timing = false;
-    std::vector<TimedLaunch> pending;
-};
-
-namespace {
-
-uint64_t pool_key(uint64_t kind, size_t bytes) { return (kind << 56) | (uint64_t)bytes; }
-
-// A buffer borrowed from the pool for the duration of one call. Reuse on the
-// stream of the last use is ordered by that stream. Once a context sees a
-// second stream, releases record an event that a user on another stream
-// waits for; at that first switch the device is synchronized once, since the
-// earlier uses recorded none. Either way reuse never races queued work.
-class Lease {
-  public:
-    Lease() = default;
-    Lease(const Lease&) = delete;
-    Lease& operator=(const Lease&) = delete;
-    ~Lease() { release(); }
-
-    int acquire(drh_ctx* ctx, uint64_t kind, size_t bytes, hipStream_t s) {
-        ctx_ = ctx;
-        kind_ = kind;
-        stream_ = s;
-        if (bytes == 0) return DRH_OK;
-        {
-            std::lock_guard<std::mutex> g(ctx->mu);
-            auto it = ctx->free_bufs.find(pool_key(kind, bytes));
-            if (it != ctx->free_bufs.end() && !it->second.empty()) {
-                buf_ = it->second.back();
-                it->second.pop_back();
-                ctx->bytes -= bytes;
-                ctx->hits += 1;
+int Lease::acquire(drh_ctx* ctx, uint64_t kind, size_t bytes, hipStream_t s) {
+    ctx_ = ctx;
+    kind_ = kind;
+    stream_ = s;
+    if (bytes == 0) return DRH_OK;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        auto it = ctx->free_bufs.find(pool_key(kind, bytes));
+        if (it != ctx->free_bufs.end() && !it->second.empty()) {
+            buf_ = it->second.back();
+            it->second.pop_back();
+            ctx->bytes -= bytes;
+            ctx->hits += 1;
+        }
+    }
+    if (buf_.ptr) {
+        if (buf_.used && buf_.stream != s) {
+            if (buf_.ev_recorded) {
+                hipError_t e = hipStreamWaitEvent(s, buf_.ev, 0);
+                if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+            } else {
+                hipError_t e = hipDeviceSynchronize();
+                if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
             }
-        }
-        if (buf_.ptr) {
-            if (buf_.used && buf_.stream != s) {
-                if (buf_.ev_recorded) {
-                    hipError_t e = hipStreamWaitEvent(s, buf_.ev, 0);
-                    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
-                } else {
-                    hipError_t e = hipDeviceSynchronize();
-                    if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-                }
-                std::lock_guard<std::mutex> g(ctx->mu);
-                ctx->multi_stream = true;
-            }
-            return DRH_OK;
-        }
-        {
             std::lock_guard<std::mutex> g(ctx->mu);
-            ctx->misses += 1;
+            ctx->multi_stream = true;
         }
-        fresh_ = true;
-        hipError_t e = hipMalloc(&buf_.ptr, bytes);
-        if (e != hipSuccess) {
-            buf_.ptr = nullptr;
-            return fail(e == hipErrorOutOfMemory ? DRH_ERR_TOO_LARGE : DRH_ERR_DEVICE,
-                        std::string("hipMalloc of ") + std::to_string(bytes) + " bytes: " + hipGetErrorString(e));
-        }
-        buf_.bytes = bytes;
-        e = hipEventCreateWithFlags(&buf_.ev, hipEventDisableTiming);
-        if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
         return DRH_OK;
     }
-
-    template <class T>
-    T* get() const {
-        return static_cast<T*>(buf_.ptr);
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        ctx->misses += 1;
     }
-    // The buffer was allocated by this lease (its contents are undefined).
-    bool fresh() const { return fresh_; }
+    hipError_t e = hipMalloc(&buf_.ptr, bytes);
+    if (e != hipSuccess) {
+        buf_.ptr = nullptr;
+        return fail(e == hipErrorOutOfMemory ? DRH_ERR_TOO_LARGE : DRH_ERR_DEVICE,
+                    std::string("hipMalloc of ") + std::to_string(bytes) + " bytes: " + hipGetErrorString(e));
+    }
+    buf_.bytes = bytes;
+    e = hipEventCreateWithFlags(&buf_.ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    return DRH_OK;
+}
 
-    void release() {
-        if (!buf_.ptr) return;
-        bool multi;
-        {
-            std::lock_guard<std::mutex> g(ctx_->mu);
-            multi = ctx_->multi_stream;
+void Lease::release() {
+    if (!buf_.ptr) return;
+    bool multi;
+    {
+        std::lock_guard<std::mutex> g(ctx_->mu);
+        multi = ctx_->multi_stream;
+    }
+    buf_.ev_recorded = multi && hipEventRecord(buf_.ev, stream_) == hipSuccess;
+    buf_.stream = stream_;
+    buf_.used = true;
+    bool keep = false;
+    {
+        std::lock_guard<std::mutex> g(ctx_->mu);
+        if (ctx_->bytes + buf_.bytes <= POOL_BYTE_LIMIT) {
+            ctx_->bytes += buf_.bytes;
+            ctx_->free_bufs[pool_key(kind_, buf_.bytes)].push_back(buf_);
+            keep = true;
         }
-        buf_.ev_recorded = multi && hipEventRecord(buf_.ev, stream_) == hipSuccess;
-        buf_.stream = stream_;
-        buf_.used = true;
-        bool keep = false;
-        {
-            std::lock_guard<std::mutex> g(ctx_->mu);
-            if (ctx_->bytes + buf_.bytes <= POOL_BYTE_LIMIT) {
-                ctx_->bytes += buf_.bytes;
-                ctx_->free_bufs[pool_key(kind_, buf_.bytes)].push_back(buf_);
-                keep = true;
-            }
-        }
-        if (!keep) {
-            // the queued work that uses the buffer finishes before it is freed
-            if (buf_.ev_recorded)
-                (void)hipEventSynchronize(buf_.ev);
-            else
-                (void)hipStreamSynchronize(stream_);
-            (void)hipEventDestroy(buf_.ev);
-            (void)hipFree(buf_.ptr);
-        }
-        buf_ = PoolBuf{};
     }
-
-  private:
-    bool fresh_ = false;
-    drh_ctx* ctx_ = nullptr;
-    uint64_t kind_ = 0;
-    hipStream_t stream_ = nullptr;
-    PoolBuf buf_;
-};
-
-// Restores the caller's current device on scope exit.
-struct DeviceGuard {
-    int prev = -1;
-    bool ok = true;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    if (!keep) {
+        // the queued work that uses the buffer finishes before it is freed
+        if (buf_.ev_recorded)
+            (void)hipEventSynchronize(buf_.ev);
+        else
+            (void)hipStreamSynchronize(stream_);
+        (void)hipEventDestroy(buf_.ev);
+        (void)hipFree(buf_.ptr);
     }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
+    buf_ = PoolBuf{};
+}
 
-// Host wait bounded like GpuRasterizer::POLL_TIMEOUT.
 int wait_stream(hipStream_t s) {
     hipEvent_t ev;
     hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
@@ -254,8 +142,6 @@ int wait_stream(hipStream_t s) {
     return DRH_OK;
 }
 
-// Argument checks shared by the raster entry points, with the reference
-// binding's messages (crates/diffrast-py/src/lib.rs:162-195).
 int check_sizes(int64_t B, int64_t T, int64_t H, int64_t W) {
     if (B < 0 || T < 0 || H < 0 || W < 0) return fail(DRH_ERR_INVALID_ARG, "sizes must be non-negative");
     if (H == 0 || W == 0) return fail(DRH_ERR_INVALID_ARG, "height and width must be non-zero");
@@ -272,12 +158,6 @@ int check_shape(drh_ctx* ctx, int64_t B, int64_t T, int64_t H, int64_t W, float 
     return check_sizes(B, T, H, W);
 }
 
-struct Staged {
-    Lease lease;
-    const float* dev = nullptr;
-};
-
-// Device view of an input array: the pointer itself, or a pooled copy.
 int stage_in(drh_ctx* ctx, Staged& st, uint64_t kind, const float* src, size_t n, bool host, hipStream_t s) {
     if (n == 0) {
         st.dev = src;
@@ -294,13 +174,6 @@ int stage_in(drh_ctx* ctx, Staged& st, uint64_t kind, const float* src, size_t n
     st.dev = st.lease.get<float>();
     return DRH_OK;
 }
-
-struct Out {
-    Lease lease;
-    float* dev = nullptr;
-    float* host_dst = nullptr;
-    size_t n = 0;
-};
 
 int stage_out(drh_ctx* ctx, Out& o, uint64_t kind, float* dst, size_t n, bool host, hipStream_t s) {
     o.n = n;
@@ -331,8 +204,6 @@ int finish(uint32_t flags, hipStream_t s) {
     return DRH_OK;
 }
 
-// f32::powi with a runtime exponent (square-and-multiply, as the
-// compiler-builtins __powisf2 that the reference's Adam calls).
 float powi_f32(float a, int32_t b) {
     bool recip = b < 0;
     float r = 1.0f;
@@ -345,46 +216,26 @@ float powi_f32(float a, int32_t b) {
     return recip ? 1.0f / r : r;
 }
 
-// fit.rs:343-349
-float sigma_at(const drh_fit_config* c, int64_t i) {
-    if (c->iters <= 1) return c->sigma_end;
-    float t = (float)i / (float)(c->iters - 1);
-    return c->sigma_start * std::pow(c->sigma_end / c->sigma_start, t);
+KernelTimer::KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s, bool enabled) : ctx_(ctx), s_(s) {
+    if (!enabled || !ctx->timing) return;
+    l_.kernel = kernel;
+    if (hipEventCreate(&l_.start) != hipSuccess || hipEventCreate(&l_.stop) != hipSuccess) return;
+    on_ = hipEventRecord(l_.start, s) == hipSuccess;
 }
 
-// Brackets one kernel launch with events when the context is timing.
-class KernelTimer {
-  public:
-    KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s) : ctx_(ctx), s_(s) {
-        if (!ctx->timing) return;
-        l_.kernel = kernel;
-        if (hipEventCreate(&l_.start) != hipSuccess || hipEventCreate(&l_.stop) != hipSuccess) return;
-        on_ = hipEventRecord(l_.start, s) == hipSuccess;
-    }
-    ~KernelTimer() {
-        if (!on_) return;
-        (void)hipEventRecord(l_.stop, s_);
-        std::lock_guard<std::mutex> g(ctx_->mu);
-        ctx_->pending.push_back(l_);
-    }
+KernelTimer::~KernelTimer() {
+    if (!on_) return;
+    (void)hipEventRecord(l_.stop, s_);
+    std::lock_guard<std::mutex> g(ctx_->mu);
+    ctx_->pending.push_back(l_);
+}
 
-  private:
-    drh_ctx* ctx_;
-    hipStream_t s_;
-    TimedLaunch l_{};
-    bool on_ = false;
-};
-
-// Entries the forward kernel records per tile: all T (the backward kernel then
-// needs no rebuild path) while that fits TILE_ENT_BUDGET bytes, else as many as
-// fit, at least CAP2_MIN. DRH_MAX_TILE_ENTRIES (environment) lowers the cap, so
-// tests can force the rebuild path.
-constexpr size_t TILE_ENT_BUDGET = 1ull << 30;
-
-int tile_entries(size_t ntiles, int T) {
+// All T entries per tile (the backward kernel then needs no rebuild path)
+// while that fits the budget, else as many as fit, at least min_cap.
+int tile_entries(size_t ntiles, int T, size_t budget, size_t min_cap) {
     size_t cap = (size_t)(T > 0 ? T : 1);
-    const size_t fit = TILE_ENT_BUDGET / (ntiles * sizeof(drh::TileEnt));
-    if (cap > fit) cap = fit > (size_t)drh::CAP2_MIN ? fit : (size_t)drh::CAP2_MIN;
+    const size_t fit = budget / (ntiles * sizeof(drh::TileEnt));
+    if (cap > fit) cap = fit > min_cap ? fit : min_cap;
     if (const char* e = std::getenv("DRH_MAX_TILE_ENTRIES")) {
         const long v = std::strtol(e, nullptr, 10);
         if (v >= 1 && (size_t)v < cap) cap = (size_t)v;
@@ -396,50 +247,31 @@ int tile_entries(size_t ntiles, int T) {
 // whose grid has more blocks than the device has CUs (with fewer, every block
 // has a CU to itself) and whose scenes' difference grids fit in LDS. A single
 // scene is left in launch order: one workgroup would make its whole order,
-// which costs about what it saves on one scene's kernels. The forward kernel follows it when
-// its lists are short (T <= FWD_ORDER_MAX_T), so that the overlap count sets its
-// cost; with longer lists every block spends about the same building them, and
-// the order only costs it locality. The backward kernel always follows it.
-constexpr int FWD_ORDER_MAX_T = 256;
-
+// which costs about what it saves on one scene's kernels. The forward kernel
+// follows it when its lists are short (T <= FWD_ORDER_MAX_T), so that the
+// overlap count sets its cost; with longer lists every block spends about the
+// same building them, and the order only costs it locality. The backward
+// kernel always follows it.
 bool use_order(const drh_ctx* ctx, int B, int gx, int gy) {
     return B > 1 && (size_t)B * gx * gy > (size_t)ctx->cus &&
            (size_t)(gx + 1) * (gy + 1) <= (size_t)drh::ORD_MAX_CELLS;
 }
 
-// The shared raster sequence: records, the forward pass, and (for the
-// gradient modes) the backward pass and the partial-row reduction.
-int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
-               int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
-               hipStream_t s) {
-    bool fast = !(flags & DRH_EXACT_MATH);
-    bool det = (flags & DRH_DETERMINISTIC) != 0;
-    dim3 grid = drh::raster_grid(B, W, H);
-    int nblk = (int)(grid.x * grid.y);
-    size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pstate, tent, tn, order;
-    const int cap2 = tile_entries(ntiles, T);
-    int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
-    if (rc) return rc;
-    if (mode != drh::MODE_RENDER) {
-        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
-            return rc;
-        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
-        if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
-        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * cap2 * sizeof(drh::TileEnt), s))) return rc;
-        if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
-    }
+int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
+                    int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
+                    uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt, bool timed) {
+    const bool fast = !(flags & DRH_EXACT_MATH);
+    const bool det = (flags & DRH_DETERMINISTIC) != 0;
+    const dim3 grid = drh::raster_grid(B, W, H);
+    const int nblk = (int)(grid.x * grid.y);
     drh::OrderArgs ord{};
-    if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
-        if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
-        ord = {order.get<int>(), (int)grid.x, (int)grid.y};
-    }
+    if (bufs.order) ord = {bufs.order, (int)grid.x, (int)grid.y};
     {
-        KernelTimer kt(ctx, TK_SETUP, s);
+        KernelTimer kt(ctx, TK_SETUP, s, timed);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
-                                  mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, rec.get<float>(),
+                                  mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, bufs.rec,
                                   mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s, nullptr, nullptr,
-                                  ord),
+                                  ord, halt),
                 "setup_records launch");
     }
     drh::RasterArgs a{};
@@ -448,48 +280,88 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     a.H = H;
     a.W = W;
     a.sigma = sigma;
-    a.rec = rec.get<float>();
+    a.rec = bufs.rec;
     a.bg = bgs;
     a.target = mode == drh::MODE_LOSS ? img_in : nullptr;
     a.grad_in = mode == drh::MODE_GRAD_IN ? img_in : nullptr;
     a.out_img = out_img;
-    a.partials = partials.get<float>();
-    a.partial_loss = ploss.get<double>();
-    a.pstate = pstate.get<drh::PixState>();
-    a.tl_ent = tent.get<drh::TileEnt>();
-    a.cap2 = cap2;
-    a.tl_n = tn.get<int>();
+    a.partials = bufs.partials;
+    a.partial_loss = bufs.ploss;
+    a.pstate = bufs.pstate;
+    a.tl_ent = bufs.tent;
+    a.cap2 = bufs.cap2;
+    a.tl_n = bufs.tn;
     a.grads = out_grads;
     a.losses = out_losses;
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
     a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     a.perm_bwd = ord.perm;
+    a.halt = halt;
     {
-        KernelTimer kt(ctx, TK_RASTER, s);
+        KernelTimer kt(ctx, TK_RASTER, s, timed);
         HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
     }
-    if (mode != drh::MODE_RENDER) {
-        {
-            KernelTimer kt(ctx, TK_BACKWARD, s);
-            HIP_TRY(drh::launch_backward(mode, fast, cap2 < T, a, s), "backward_kernel launch");
-        }
-        if (!det) return DRH_OK;
-        KernelTimer kt(ctx, TK_REDUCE, s);
-        HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3 * H * W, out_grads,
-                                   mode == drh::MODE_LOSS ? out_losses : nullptr, s),
-                "reduce_partials launch");
+    if (mode == drh::MODE_RENDER) return DRH_OK;
+    {
+        KernelTimer kt(ctx, TK_BACKWARD, s, timed);
+        HIP_TRY(drh::launch_backward(mode, fast, bufs.cap2 < T, a, s), "backward_kernel launch");
     }
+    if (!det) return DRH_OK;
+    KernelTimer kt(ctx, TK_REDUCE, s, timed);
+    HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3.0 * (double)H * (double)W, out_grads,
+                               mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
+            "reduce_partials launch");
     return DRH_OK;
 }
 
+int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
+               int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
+               hipStream_t s, const int* halt) {
+    const bool det = (flags & DRH_DETERMINISTIC) != 0;
+    const dim3 grid = drh::raster_grid(B, W, H);
+    const int nblk = (int)(grid.x * grid.y);
+    const size_t ntiles = (size_t)B * nblk * drh::WAVES;
+    Lease rec, partials, ploss, pstate, tent, tn, order;
+    RasterBufs bufs;
+    bufs.cap2 = tile_entries(ntiles, T);
+    int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
+    if (rc) return rc;
+    if (mode != drh::MODE_RENDER) {
+        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
+            return rc;
+        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
+        if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
+        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
+        if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
+    }
+    if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
+        if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
+        bufs.order = order.get<int>();
+    }
+    bufs.rec = rec.get<float>();
+    bufs.partials = partials.get<float>();
+    bufs.ploss = ploss.get<double>();
+    bufs.pstate = pstate.get<drh::PixState>();
+    bufs.tent = tent.get<drh::TileEnt>();
+    bufs.tn = tn.get<int>();
+    return run_raster_bufs(ctx, mode, params, bgs, img_in, B, T, H, W, sigma, out_img, out_grads, out_losses, flags,
+                           bufs, s, halt);
+}
+
+}  // namespace drh_rt
+
+namespace {
+
+using namespace drh_rt;
+
 // The forward record that drh_render_record leaves for drh_backward_recorded,
-// in device memory the caller owns: the triangle records, a copy of the
-// backgrounds, the per-pixel hand-over, the per-tile entries (with their
-// counts) and the backward kernel's block order, each starting at a 256-byte
-// boundary.
+// in device memory the caller owns: a head (sizes, sigma, math mode), the
+// triangle records, a copy of the backgrounds, the per-pixel hand-over, the
+// per-tile entries (with their counts) and the backward kernel's block order,
+// each starting at a 256-byte boundary.
 struct RecordLayout {
-    size_t rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, ord = 0, total = 0;
+    size_t head = 0, rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, ord = 0, total = 0;
     int cap2 = 0;
 };
 
@@ -501,6 +373,8 @@ RecordLayout record_layout(int64_t B, int64_t T, int64_t H, int64_t W) {
     L.cap2 = tile_entries(ntiles, (int)T);
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     size_t off = 0;
+    L.head = off;
+    off = up(off + sizeof(drh::RecordHead));
     L.rec = off;
     off = up(off + (size_t)B * T * drh::REC * sizeof(float));
     L.bg = off;
@@ -527,11 +401,59 @@ int check_record(const void* record, uint64_t record_bytes, const RecordLayout& 
     return DRH_OK;
 }
 
-}  // namespace
+drh::RecordHead make_head(int64_t B, int64_t T, int64_t H, int64_t W, float sigma, uint32_t flags) {
+    drh::RecordHead h{};
+    h.magic = drh::RECORD_MAGIC;
+    h.exact = (flags & DRH_EXACT_MATH) ? 1u : 0u;
+    h.sigma = sigma;
+    h.B = (int32_t)B;
+    h.T = (int32_t)T;
+    h.H = (int32_t)H;
+    h.W = (int32_t)W;
+    return h;
+}
+
+// Records remembered per context; past this many the registry starts over
+// (a record it no longer knows has its head read from the device).
+constexpr size_t RECORD_REGISTRY_MAX = 4096;
+
+void remember_record(drh_ctx* ctx, const void* record, const drh::RecordHead& h) {
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (ctx->records.size() >= RECORD_REGISTRY_MAX && !ctx->records.count(record)) ctx->records.clear();
+    ctx->records[record] = h;
+}
+
+// The backward of a record must run with the forward's sizes, sigma and math
+// mode: the record's masks and transmittance totals were made with them.
+int check_record_head(drh_ctx* ctx, const void* record, const drh::RecordHead& want, hipStream_t s) {
+    drh::RecordHead have{};
+    bool known = false;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        auto it = ctx->records.find(record);
+        if (it != ctx->records.end()) {
+            have = it->second;
+            known = true;
+        }
+    }
+    if (!known) {
+        HIP_TRY(hipMemcpyAsync(&have, record, sizeof have, hipMemcpyDeviceToHost, s), "read record head");
+        int rc = wait_stream(s);
+        if (rc) return rc;
+        if (have.magic != drh::RECORD_MAGIC)
+            return fail(DRH_ERR_INVALID_ARG, "record was not written by drh_render_record");
+    }
+    if (have.B != want.B || have.T != want.T || have.H != want.H || have.W != want.W)
+        return fail(DRH_ERR_INVALID_ARG, "record was made for other sizes (B, T, H, W)");
+    if (have.sigma != want.sigma)
+        return fail(DRH_ERR_INVALID_ARG, "sigma differs from the sigma of the record's forward pass");
+    if (have.exact != want.exact)
+        return fail(DRH_ERR_INVALID_ARG, "DRH_EXACT_MATH differs from the record's forward pass");
+    return DRH_OK;
+}
 
 // ---------------------------------------------------------------- sRGB bytes
 
-namespace {
 
 // canvas.rs:100-105, with the reference's f32 operations in its order (no
 // contraction: the library is built with -ffp-contract=off) and the host
@@ -591,7 +513,7 @@ const SrgbTables& srgb_tables() {
 
 extern "C" {
 
-const char* drh_last_error(void) { return g_err.c_str(); }
+const char* drh_last_error(void) { return last_error_text(); }
 
 int drh_params_per_triangle(void) { return NP; }
 
@@ -814,9 +736,12 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     a.perm_fwd = a.T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     {
         KernelTimer kt(ctx, TK_SETUP, s);
+        const drh::RecordHead head = make_head(B, T, H, W, sigma, flags);
         HIP_TRY(drh::launch_setup(p.dev, a.B, a.T, a.W, a.H, sigma, drh::SETUP_RECORD, const_cast<float*>(a.rec),
-                                  nullptr, s, bg.dev, const_cast<float*>(a.bg), ord),
+                                  nullptr, s, bg.dev, const_cast<float*>(a.bg), ord, nullptr,
+                                  reinterpret_cast<drh::RecordHead*>(base + L.head), head),
                 "setup_records launch");
+        remember_record(ctx, record, head);
     }
     {
         KernelTimer kt(ctx, TK_RASTER, s);
@@ -837,6 +762,7 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     if ((rc = check_record(record, record_bytes, L))) return rc;
     DeviceGuard dg(ctx->device);
     hipStream_t s = (hipStream_t)stream;
+    if ((rc = check_record_head(ctx, record, make_head(B, T, H, W, sigma, flags), s))) return rc;
     const bool host = flags & DRH_HOST_PTRS;
     const bool det = (flags & DRH_DETERMINISTIC) != 0;
     Staged gi;
@@ -879,7 +805,7 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     }
     if (det) {
         KernelTimer kt(ctx, TK_REDUCE, s);
-        HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, a.T, 3 * a.H * a.W, grads.dev, nullptr, s),
+        HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, a.T, 3.0 * a.H * (double)a.W, grads.dev, nullptr, s),
                 "reduce_partials launch");
     }
     if ((rc = copy_back(grads, s))) return rc;
@@ -970,114 +896,6 @@ int drh_decode_srgb(drh_ctx* ctx, const uint8_t* bytes, int64_t n, float* out, v
     HIP_TRY(drh::launch_decode_srgb(din, n, o.dev, srgb_tables().values, s), "decode_srgb launch");
     if ((rc = copy_back(o, s))) return rc;
     return finish(flags, s);
-}
-
-int drh_fit_validate(const drh_fit_config* c, int64_t T) {
-    if (!c) return fail(DRH_ERR_INVALID_ARG, "config is NULL");
-    // fit.rs:98-117, in the reference's order, with its messages (fit.rs:34-44).
-    if (T <= 0) return (void)fail(DRH_ERR_INVALID_ARG, "triangles must be greater than zero"), DRH_CFG_NO_TRIANGLES;
-    if (!(std::isfinite(c->sigma_start) && std::isfinite(c->sigma_end)) || c->sigma_start <= 0.0f ||
-        c->sigma_end <= 0.0f)
-        return (void)fail(DRH_ERR_INVALID_ARG, "sigma_start and sigma_end must be positive and finite"),
-               DRH_CFG_NON_POSITIVE_SIGMA;
-    if (c->sigma_start < c->sigma_end)
-        return (void)fail(DRH_ERR_INVALID_ARG, "sigma_start must be greater than or equal to sigma_end"),
-               DRH_CFG_SIGMA_NOT_DECREASING;
-    for (float lr : {c->lr_pos, c->lr_color, c->lr_alpha})
-        if (!std::isfinite(lr) || lr <= 0.0f)
-            return (void)fail(DRH_ERR_INVALID_ARG, "learning rates must be positive and finite"),
-                   DRH_CFG_NON_POSITIVE_LEARNING_RATE;
-    return DRH_CFG_OK;
-}
-
-int drh_fit(drh_ctx* ctx, const float* target, int64_t H, int64_t W, const float* background,
-            const float* init_params, int64_t T, const drh_fit_config* cfg, float* out_losses,
-            float* out_best_params, float* out_params, drh_fit_report* report, void* stream, uint32_t flags) {
-    if (!ctx) return fail(DRH_ERR_INVALID_ARG, "context is NULL");
-    if (drh_fit_validate(cfg, T) != DRH_CFG_OK) return DRH_ERR_INVALID_ARG;
-    int rc = check_shape(ctx, 1, T, H, W, cfg->sigma_end);
-    if (rc) return rc;
-    if (cfg->iters < 0 || cfg->iters > INT32_MAX) return fail(DRH_ERR_INVALID_ARG, "bad iteration count");
-    if (!report || !out_best_params || (cfg->iters > 0 && !out_losses) || !background || !target || !init_params)
-        return fail(DRH_ERR_INVALID_ARG, "NULL argument");
-    DeviceGuard dg(ctx->device);
-    hipStream_t s = (hipStream_t)stream;
-    bool host = flags & DRH_HOST_PTRS;
-    const int n = (int)(T * NP);
-    Staged tg, bg, init;
-    if ((rc = stage_in(ctx, tg, K_IN_IMAGES, target, (size_t)H * W * 3, host, s))) return rc;
-    if ((rc = stage_in(ctx, bg, K_IN_BG, background, 3, host, s))) return rc;
-    if ((rc = stage_in(ctx, init, K_IN_PARAMS, init_params, (size_t)n, host, s))) return rc;
-
-    // Working set: params, m, v, lr, grads, best, losses, loss; one lease.
-    const size_t iters = (size_t)cfg->iters;
-    const size_t f32s = (size_t)n * 6 + iters + 1;
-    Lease work, state;
-    if ((rc = work.acquire(ctx, K_FIT_F32, f32s * sizeof(float), s))) return rc;
-    if ((rc = state.acquire(ctx, K_FIT_STATE, sizeof(drh::FitState), s))) return rc;
-    float* d_params = work.get<float>();
-    float* d_m = d_params + n;
-    float* d_v = d_m + n;
-    float* d_lr = d_v + n;
-    float* d_grads = d_lr + n;
-    float* d_best = d_grads + n;
-    float* d_losses = d_best + n;
-    float* d_loss = d_losses + iters;
-    drh::FitState* d_st = state.get<drh::FitState>();
-
-    // fit.rs:388-396 learning_rates()
-    std::vector<float> lr((size_t)n);
-    for (int64_t k = 0; k < T; k++) {
-        for (int j = 0; j < 6; j++) lr[k * NP + j] = cfg->lr_pos;
-        for (int j = 6; j < 9; j++) lr[k * NP + j] = cfg->lr_color;
-        lr[k * NP + 9] = cfg->lr_alpha;
-    }
-    drh::FitState st0{INFINITY, 0, 0, 0, -1};
-    HIP_TRY(hipMemcpyAsync(d_params, init.dev, n * sizeof(float), hipMemcpyDeviceToDevice, s), "copy init");
-    HIP_TRY(hipMemcpyAsync(d_best, init.dev, n * sizeof(float), hipMemcpyDeviceToDevice, s), "copy init");
-    HIP_TRY(hipMemsetAsync(d_m, 0, 2 * n * sizeof(float), s), "zero moments");
-    HIP_TRY(hipMemcpyAsync(d_lr, lr.data(), n * sizeof(float), hipMemcpyHostToDevice, s), "upload lr");
-    HIP_TRY(hipMemcpyAsync(d_st, &st0, sizeof st0, hipMemcpyHostToDevice, s), "upload state");
-    HIP_TRY(hipStreamSynchronize(s), "fit setup");  // lr / st0 are stack memory
-
-    const float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f;  // optim.rs:29-31
-    drh::FitState probe{};
-    for (int64_t i = 0; i < (int64_t)iters; i++) {
-        float sigma = sigma_at(cfg, i);
-        // Fixed-order gradient sums: a fit with a given start is reproducible,
-        // as the reference's is (fit.rs:487-496).
-        if ((rc = run_raster(ctx, drh::MODE_LOSS, d_params, bg.dev, tg.dev, 1, (int)T, (int)H, (int)W, sigma,
-                             nullptr, d_grads, d_loss, (flags & ~DRH_CHANNELS_FIRST) | DRH_DETERMINISTIC, s)))
-            return rc;
-        int32_t t = (int32_t)(i + 1);
-        float bc1 = 1.0f - powi_f32(beta1, t), bc2 = 1.0f - powi_f32(beta2, t);
-        {
-            KernelTimer kt(ctx, TK_ADAM, s);
-            HIP_TRY(drh::launch_fit_tail((int)i, d_loss, d_params, d_grads, d_m, d_v, d_lr, n, beta1, beta2, eps,
-                                         bc1, bc2, cfg->min_delta, cfg->patience, d_st, d_losses, d_best, s),
-                    "fit_tail launch");
-        }
-        // Stop launching once the device has stopped; checked now and then
-        // rather than per step, so the loop has no per-step host round trip.
-        if ((i & 63) == 63) {
-            HIP_TRY(hipMemcpyAsync(&probe, d_st, sizeof probe, hipMemcpyDeviceToHost, s), "read state");
-            if ((rc = wait_stream(s))) return rc;
-            if (probe.stop >= 0) break;
-        }
-    }
-    drh::FitState fin{};
-    HIP_TRY(hipMemcpyAsync(&fin, d_st, sizeof fin, hipMemcpyDeviceToHost, s), "read state");
-    if ((rc = wait_stream(s))) return rc;
-    hipMemcpyKind k = host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
-    if (fin.n_losses > 0) HIP_TRY(hipMemcpyAsync(out_losses, d_losses, fin.n_losses * sizeof(float), k, s), "copy losses");
-    HIP_TRY(hipMemcpyAsync(out_best_params, d_best, n * sizeof(float), k, s), "copy best");
-    if (out_params) HIP_TRY(hipMemcpyAsync(out_params, d_params, n * sizeof(float), k, s), "copy params");
-    if ((rc = wait_stream(s))) return rc;
-    report->n_losses = fin.n_losses;
-    report->best_iter = fin.best_iter;
-    report->best_loss = fin.best_loss;
-    report->stop_reason = fin.stop < 0 ? DRH_STOP_COMPLETED : fin.stop;
-    return DRH_OK;
 }
 
 }  // extern "C"

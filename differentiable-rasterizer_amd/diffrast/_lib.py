@@ -86,6 +86,21 @@ class Timings(ctypes.Structure):
     ]
 
 
+class StepInfo(ctypes.Structure):
+    _fields_ = [("iter", ctypes.c_int64), ("loss", ctypes.c_float), ("sigma", ctypes.c_float)]
+
+
+class FitStatus(ctypes.Structure):
+    _fields_ = [
+        ("iter", ctypes.c_int64),
+        ("best_iter", ctypes.c_int64),
+        ("best_loss", ctypes.c_float),
+        ("sigma", ctypes.c_float),
+        ("done", ctypes.c_int32),
+        ("stop_reason", ctypes.c_int32),
+    ]
+
+
 # Every symbol include/diffrast_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "drh_timing_enable": ([_P, ctypes.c_int], ctypes.c_int),
@@ -108,6 +123,16 @@ SIGNATURES = {
     "drh_fit_validate": ([ctypes.POINTER(FitConfig), _I64], ctypes.c_int),
     "drh_fit": ([_P, _P, _I64, _I64, _P, _P, _I64, ctypes.POINTER(FitConfig), _P, _P, _P,
                  ctypes.POINTER(FitReport), _P, _U32], ctypes.c_int),
+    "drh_fitter_create": ([_P, _P, _I64, _I64, _P, _P, _I64, ctypes.POINTER(FitConfig), _P, _U32,
+                           ctypes.POINTER(_P)], ctypes.c_int),
+    "drh_fitter_destroy": ([_P], ctypes.c_int),
+    "drh_fitter_step": ([_P, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(StepInfo)], ctypes.c_int),
+    "drh_fitter_run": ([_P, _I64, ctypes.POINTER(_I64)], ctypes.c_int),
+    "drh_fitter_status": ([_P, ctypes.POINTER(FitStatus)], ctypes.c_int),
+    "drh_fitter_scene": ([_P, _P, _U32], ctypes.c_int),
+    "drh_fitter_losses": ([_P, _P, _I64, ctypes.POINTER(_I64), _U32], ctypes.c_int),
+    "drh_fitter_render_current": ([_P, _P, _U32], ctypes.c_int),
+    "drh_fitter_report": ([_P, _P, ctypes.POINTER(FitReport), _U32], ctypes.c_int),
     "drh_record_bytes": ([_I64, _I64, _I64, _I64, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "drh_render_record": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, ctypes.c_uint64, _P, _U32],
                           ctypes.c_int),
@@ -339,13 +364,96 @@ class Context:
                     stop_reason=STOP_REASONS[rep.stop_reason])
 
 
+FIT_DEFAULTS = dict(iters=1500, sigma_start=0.02, sigma_end=0.0015, lr_pos=0.004, lr_color=0.02,
+                    lr_alpha=0.01, patience=250, min_delta=1e-7)  # FitConfig::default (fit.rs:67-89)
+
+
+def _fit_config(**cfg) -> FitConfig:
+    c = dict(FIT_DEFAULTS)
+    c.update(cfg)
+    return FitConfig(c["iters"], c["sigma_start"], c["sigma_end"], c["lr_pos"], c["lr_color"], c["lr_alpha"],
+                     -1 if c["patience"] is None else int(c["patience"]), c["min_delta"])
+
+
+class Fitter:
+    """Fitter (fit.rs:191-335) on the device, from a given initial scene.
+
+    `step()` runs one iteration and returns its StepInfo as a dict (None once
+    the fit has stopped, for any reason); `run(n)` runs up to n iterations
+    without waiting between them. The state lives on the device."""
+
+    def __init__(self, ctx: Context, target, init_params, background, exact: bool = False, **cfg):
+        t = _f32(target)
+        self.H, self.W = t.shape[0], t.shape[1]
+        p = _f32(init_params).reshape(-1, 10)
+        self.T = p.shape[0]
+        bg = _f32(background).reshape(3)
+        self.cfg = _fit_config(**cfg)
+        self._ctx = ctx  # the context must outlive the fitter
+        h = ctypes.c_void_p()
+        check(lib().drh_fitter_create(ctx.handle, _ptr(t), self.H, self.W, _ptr(bg), _ptr(p), self.T,
+                                      ctypes.byref(self.cfg), None, HOST_PTRS | (EXACT_MATH if exact else 0),
+                                      ctypes.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            lib().drh_fitter_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def step(self):
+        stepped = ctypes.c_int()
+        info = StepInfo()
+        check(lib().drh_fitter_step(self.handle, ctypes.byref(stepped), ctypes.byref(info)))
+        if not stepped.value:
+            return None
+        return dict(iter=int(info.iter), loss=float(info.loss), sigma=float(info.sigma))
+
+    def run(self, max_steps: int) -> int:
+        ran = ctypes.c_int64()
+        check(lib().drh_fitter_run(self.handle, max_steps, ctypes.byref(ran)))
+        return int(ran.value)
+
+    def status(self) -> dict:
+        s = FitStatus()
+        check(lib().drh_fitter_status(self.handle, ctypes.byref(s)))
+        return dict(iter=int(s.iter), best_iter=int(s.best_iter), best_loss=float(s.best_loss),
+                    sigma=float(s.sigma), done=bool(s.done),
+                    stop_reason=None if s.stop_reason < 0 else STOP_REASONS[s.stop_reason])
+
+    def scene(self) -> np.ndarray:
+        out = np.empty((self.T, 10), np.float32)
+        check(lib().drh_fitter_scene(self.handle, _ptr(out), HOST_PTRS))
+        return out
+
+    def losses(self) -> np.ndarray:
+        n = ctypes.c_int64()
+        out = np.empty(max(int(self.cfg.iters), 1), np.float32)
+        check(lib().drh_fitter_losses(self.handle, _ptr(out), out.size, ctypes.byref(n), HOST_PTRS))
+        return out[: n.value].copy()
+
+    def render_current(self) -> np.ndarray:
+        out = np.empty((self.H, self.W, 3), np.float32)
+        check(lib().drh_fitter_render_current(self.handle, _ptr(out), HOST_PTRS))
+        return out
+
+    def into_report(self) -> dict:
+        best = np.empty((self.T, 10), np.float32)
+        rep = FitReport()
+        check(lib().drh_fitter_report(self.handle, _ptr(best), ctypes.byref(rep), HOST_PTRS))
+        return dict(best_params=best, losses=self.losses(), best_iter=int(rep.best_iter),
+                    best_loss=float(rep.best_loss), stop_reason=STOP_REASONS[rep.stop_reason])
+
+
 def validate_fit_config(T: int, **cfg) -> str | None:
     """FitConfig::validate (fit.rs:98-117): None when valid, else the error name."""
-    c = dict(iters=1500, sigma_start=0.02, sigma_end=0.0015, lr_pos=0.004, lr_color=0.02,
-             lr_alpha=0.01, patience=250, min_delta=1e-7)
-    c.update(cfg)
-    conf = FitConfig(c["iters"], c["sigma_start"], c["sigma_end"], c["lr_pos"], c["lr_color"],
-                     c["lr_alpha"], -1 if c["patience"] is None else c["patience"], c["min_delta"])
+    conf = _fit_config(**cfg)
     rc = lib().drh_fit_validate(ctypes.byref(conf), T)
     return CONFIG_ERRORS.get(rc)
 

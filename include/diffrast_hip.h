@@ -145,8 +145,9 @@ int drh_render_record(drh_ctx *ctx, const float *params, const float *background
 
 /* drh_backward_from_grad for the scenes of a drh_render_record call, from its
  * record, without rendering again: B, T, H, W, sigma and DRH_EXACT_MATH must be
- * those of that call (DRH_CHANNELS_FIRST here describes grad_images). The
- * record is only read, so one record serves any number of backward calls. */
+ * those of that call, else DRH_ERR_INVALID_ARG (the record's head holds them;
+ * DRH_CHANNELS_FIRST here describes grad_images). The record is only read, so
+ * one record serves any number of backward calls. */
 int drh_backward_recorded(drh_ctx *ctx, const void *record, uint64_t record_bytes,
                           const float *grad_images, int64_t B, int64_t T, int64_t H, int64_t W,
                           float sigma, float *out_grads, void *stream, uint32_t flags);
@@ -192,16 +193,80 @@ typedef struct {
 /* FitConfig::validate (fit.rs:98-117) for a scene of T triangles. */
 int drh_fit_validate(const drh_fit_config *cfg, int64_t T);
 
-/* The fit loop (fit.rs:166-288) from a given initial scene, with every step
- * on the device: sigma annealing, fused loss and gradients, divergence, best
- * snapshot and patience bookkeeping, Adam and projection. The loss is read
- * back once at the end, not per step. target is H x W x 3, init_params and
- * out_best_params T x 10, out_losses room for cfg->iters floats,
- * out_params (optional) receives the last iterate. */
+/* The fit loop (fit.rs:166-181, the batch form `fit` without its progress
+ * callback) from a given initial scene, with every step on the device: sigma
+ * annealing, fused loss and gradients, divergence, best snapshot and patience
+ * bookkeeping, Adam and projection. The device state is read back every 64
+ * iterations and at the end, not per step; once the fit has stopped, the
+ * kernels of iterations already launched return at entry. target is
+ * H x W x 3, init_params and out_best_params T x 10, out_losses room for
+ * cfg->iters floats, out_params (optional) receives the last iterate.
+ * Equivalent to drh_fitter_create + drh_fitter_run(iters) + drh_fitter_losses
+ * + drh_fitter_report. */
 int drh_fit(drh_ctx *ctx, const float *target, int64_t H, int64_t W, const float *background,
             const float *init_params, int64_t T, const drh_fit_config *cfg, float *out_losses,
             float *out_best_params, float *out_params, drh_fit_report *report, void *stream,
             uint32_t flags);
+
+/* A fit advanced one iteration at a time: Fitter (fit.rs:191-335). Its state
+ * (scene, Adam moments, losses, best snapshot, stop reason) lives on the
+ * device; the fitter owns copies of the target and background. A fitter is
+ * used from one thread at a time and enqueues on the stream it was created
+ * with; its context must outlive it. */
+typedef struct drh_fitter drh_fitter;
+
+/* StepInfo (fit.rs:183-189). */
+typedef struct {
+    int64_t iter;
+    float loss;
+    float sigma;
+} drh_step_info;
+
+/* Fitter::{iter, best_loss, sigma, is_done} (fit.rs:299-318) and the stop
+ * reason so far (-1 while running, else DRH_STOP_*). best_iter is the
+ * iteration of the best snapshot. */
+typedef struct {
+    int64_t iter;
+    int64_t best_iter;
+    float best_loss;
+    float sigma;
+    int32_t done;
+    int32_t stop_reason;
+} drh_fit_status;
+
+/* Fitter::new (fit.rs:214-237) from a given initial scene (T x 10) instead of
+ * seed_scene's random one; DRH_ERR_INVALID_ARG for an invalid configuration
+ * (drh_fit_validate names it). flags: DRH_HOST_PTRS for host inputs,
+ * DRH_EXACT_MATH. */
+int drh_fitter_create(drh_ctx *ctx, const float *target, int64_t H, int64_t W, const float *background,
+                      const float *init_params, int64_t T, const drh_fit_config *cfg, void *stream,
+                      uint32_t flags, drh_fitter **out);
+int drh_fitter_destroy(drh_fitter *f);
+
+/* Fitter::step (fit.rs:239-288): runs one iteration and waits for its loss.
+ * *stepped = 1 and *info (optional) filled when it ran (Some), 0 once the fit
+ * has stopped, for any reason (None). */
+int drh_fitter_step(drh_fitter *f, int *stepped, drh_step_info *info);
+
+/* Up to max_steps iterations without waiting between them (the device state
+ * is read back every 64 iterations and at the end); *ran (optional) is the
+ * number of iterations recorded. */
+int drh_fitter_run(drh_fitter *f, int64_t max_steps, int64_t *ran);
+
+int drh_fitter_status(const drh_fitter *f, drh_fit_status *out);
+
+/* Fitter::scene (fit.rs:290-293): the current parameters, T x 10. */
+int drh_fitter_scene(drh_fitter *f, float *out_params, uint32_t flags);
+
+/* Fitter::losses (fit.rs:303-305): *n_out losses into out (capacity floats). */
+int drh_fitter_losses(drh_fitter *f, float *out, int64_t capacity, int64_t *n_out, uint32_t flags);
+
+/* Fitter::render_current (fit.rs:320-324): the current scene at sigma_end,
+ * H x W x 3. */
+int drh_fitter_render_current(drh_fitter *f, float *out_image, uint32_t flags);
+
+/* Fitter::into_report (fit.rs:326-334): the best scene (T x 10) and the report. */
+int drh_fitter_report(drh_fitter *f, float *out_best_params, drh_fit_report *report, uint32_t flags);
 
 /* The gamma of Canvas::save_png (crates/diffrast/src/canvas.rs:61-68):
  * encode_srgb (canvas.rs:100-105) of n linear values, in any layout, to sRGB

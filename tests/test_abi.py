@@ -81,14 +81,15 @@ def test_record_bytes_cover_every_part(L):
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     B, T, H, W = 16, 128, 256, 256
     tiles = B * (W // 8) * (H // 8)
-    want = (up(B * T * 76 * 4) + up(B * 3 * 4) + up(B * H * W * 24) + up(tiles * 8) + up(tiles * T * 24)
+    head = 256  # sizes, sigma and math mode of the forward pass
+    want = (head + up(B * T * 76 * 4) + up(B * 3 * 4) + up(B * H * W * 24) + up(tiles * 8) + up(tiles * T * 24)
             + up(tiles // 4 * 4))
     assert L.record_bytes(B, T, H, W) == want
     assert L.record_bytes(0, T, H, W) == 0
     # odd sizes count the partial tiles of whole 16x16 blocks
     tiles = 3 * 2 * 2 * 4  # 2 x 2 blocks of 2 x 2 tiles per scene
-    assert L.record_bytes(3, 5, 17, 30) == (up(3 * 5 * 76 * 4) + up(36) + up(3 * 17 * 30 * 24) + up(tiles * 8)
-                                           + up(tiles * 5 * 24) + up(tiles // 4 * 4))
+    assert L.record_bytes(3, 5, 17, 30) == (head + up(3 * 5 * 76 * 4) + up(36) + up(3 * 17 * 30 * 24)
+                                           + up(tiles * 8) + up(tiles * 5 * 24) + up(tiles // 4 * 4))
     with pytest.raises(L.DiffrastError) as e:
         L.record_bytes(1, 1, 0, 4)
     assert e.value.code == 6

@@ -1,24 +1,17 @@
-"""HIP path vs the CPU oracle, through the C ABI.
+"""HIP path vs the CPU oracle, through the C ABI, on edge cases and odd shapes.
 
-Bars (from the acceptance criteria of this path):
-  images       max |gpu - cpu| <= 1e-5
-  losses       |gpu - cpu| <= 1e-4 * |cpu|   (and 1e-7 absolute)
-  gradients    max |gpu - cpu| / ||cpu||_2 <= 1e-4 per scene, the reference's
-               own normalisation (crates/diffrast-gpu/src/lib.rs:1249-1254)
-The GPU sums per-pixel contributions in a different order than the CPU's
-serial f32 loops, so gradients are compared to a tolerance, not bitwise.
+The bars (images 1e-5, losses 1e-4 relative, gradients 1e-4 of the norm per scene
+and per parameter group) are in tests/bars.py; the benchmark configurations have
+their own tests in test_gpu_configs.py.
 """
 
 import numpy as np
 import pytest
 
+from bars import GRAD_RTOL, IMG_TOL, assert_grads, check_image, check_losses, grad_err
 from diffrast import synth
 
 pytestmark = pytest.mark.gpu
-
-IMG_TOL = 1e-5
-LOSS_RTOL = 1e-4
-GRAD_RTOL = 1e-4
 
 
 @pytest.fixture(scope="module")
@@ -31,25 +24,9 @@ def ctx():
     c.close()
 
 
-def grad_err(gpu, cpu):
-    """Per-scene max |d| / ||g_cpu||_2, worst over the batch."""
-    gpu = np.asarray(gpu, np.float64).reshape(len(gpu), -1)
-    cpu = np.asarray(cpu, np.float64).reshape(len(cpu), -1)
-    worst = 0.0
-    for a, b in zip(gpu, cpu):
-        n = max(np.linalg.norm(b), 1e-12)
-        worst = max(worst, float(np.abs(a - b).max()) / n if a.size else 0.0)
-    return worst
-
-
-def check_losses(gpu, cpu):
-    gpu, cpu = np.asarray(gpu, np.float64), np.asarray(cpu, np.float64)
-    assert np.all(np.abs(gpu - cpu) <= LOSS_RTOL * np.abs(cpu) + 1e-7), (gpu, cpu)
-
-
 CASES = [
     # (name, B, H, W, T, sigma, kind)
-    ("c0", 1, 64, 64, 32, 0.0015, "uniform"),
+    ("64x64-T32", 1, 64, 64, 32, 0.0015, "uniform"),
     ("odd-sizes", 2, 19, 37, 33, 0.02, "uniform"),
     ("tall", 1, 41, 17, 65, 0.02, "uniform"),
     ("wide-sigma", 3, 48, 40, 12, 0.05, "uniform"),
@@ -75,7 +52,7 @@ def test_render_matches_oracle(ctx, orc, name, B, H, W, T, sigma, kind, exact):
     print(f"render {name} exact={exact}", flush=True)
     gpu = ctx.render(params, H, W, sigma, bgs, exact=exact)
     cpu = orc.render_batch(params, H, W, sigma, bgs)
-    assert np.abs(gpu - cpu).max() <= IMG_TOL
+    check_image(gpu, cpu)
 
 
 @pytest.mark.parametrize("exact", [False, True], ids=["fast", "exact"])
@@ -89,7 +66,7 @@ def test_fused_loss_backward_matches_oracle(ctx, orc, name, B, H, W, T, sigma, k
     cl, cg = orc.loss_backward_batch(params, targets, sigma, bgs)
     assert np.abs(gimg - orc.render_batch(params, H, W, sigma, bgs)).max() <= IMG_TOL
     check_losses(gl, cl)
-    assert grad_err(gg, cg) <= GRAD_RTOL
+    assert_grads(gg, cg)
 
 
 @pytest.mark.parametrize("name,B,H,W,T,sigma,kind", CASES[:6], ids=[c[0] for c in CASES[:6]])
@@ -99,24 +76,11 @@ def test_backward_from_grad_matches_oracle(ctx, orc, name, B, H, W, T, sigma, ki
     print(f"from_grad {name}", flush=True)
     gpu = ctx.backward_from_grad(params, gin, sigma, bgs)
     cpu = orc.backward_from_grad_batch(params, gin, sigma, bgs)
-    assert grad_err(gpu, cpu) <= GRAD_RTOL
+    assert_grads(gpu, cpu, label=name)
     # the reference CPU binding's target-inversion route agrees to the same bar
     inv = np.stack([orc.backward_from_grad(params[b], gin[b], sigma, bgs[b], inverted=True)
                     for b in range(B)])
-    assert grad_err(gpu, inv) <= GRAD_RTOL
-
-
-def test_batch_c1_matches_oracle(ctx, orc):
-    cfg = synth.CONFIGS["c1"]
-    B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
-    params = synth.batch("uniform", B, T, 1)
-    targets = orc.render_batch(synth.batch("uniform", B, T, 1, target_offset=1000), H, W, 0.0015)
-    print("c1 parity", flush=True)
-    gl, gg = ctx.fused_loss_backward(params, targets, 0.0015)
-    cl, cg = orc.loss_backward_batch(params, targets, 0.0015)
-    check_losses(gl, cl)
-    assert grad_err(gg, cg) <= GRAD_RTOL
-    assert np.abs(ctx.render(params, H, W, 0.0015) - orc.render_batch(params, H, W, 0.0015)).max() <= IMG_TOL
+    assert_grads(gpu, inv, label=f"{name} inverted")
 
 
 def test_opaque_stack_and_clamped_alpha(ctx, orc):
@@ -129,7 +93,7 @@ def test_opaque_stack_and_clamped_alpha(ctx, orc):
     gl, gg = ctx.fused_loss_backward(params, targets, 0.003)
     cl, cg = orc.loss_backward_batch(params, targets, 0.003)
     check_losses(gl, cl)
-    assert grad_err(gg, cg) <= GRAD_RTOL
+    assert_grads(gg, cg)
     pinned = params[..., 9] >= 1.0  # a clamped alpha gets no gradient (grad.rs:144-145)
     assert pinned.sum() > 10 and np.all(gg[..., 9][pinned] == 0.0)
 
@@ -153,10 +117,9 @@ def test_deep_stack_rescales_the_transmittance(ctx, orc):
         gl, gg = ctx.fused_loss_backward(params, targets, sigma)
         cl, cg = orc.loss_backward_batch(params, targets, sigma)
         check_losses(gl, cl)
-        assert grad_err(gg, cg) <= GRAD_RTOL
+        assert_grads(gg, cg)
         gi = (targets - 0.5).astype(np.float32) * 1e-3
-        assert grad_err(ctx.backward_from_grad(params, gi, sigma),
-                        orc.backward_from_grad_batch(params, gi, sigma)) <= GRAD_RTOL
+        assert_grads(ctx.backward_from_grad(params, gi, sigma), orc.backward_from_grad_batch(params, gi, sigma))
 
 
 def test_special_triangles(ctx, orc):
@@ -178,7 +141,7 @@ def test_special_triangles(ctx, orc):
         gl, gg = ctx.fused_loss_backward(params, target, sigma)
         cl, cg = orc.loss_backward_batch(params, target, sigma)
         check_losses(gl, cl)
-        assert grad_err(gg, cg) <= GRAD_RTOL
+        assert_grads(gg, cg)
         assert np.all(gg[0, [2, 3, 4, 5, 6]] == 0.0)
 
 
@@ -194,7 +157,8 @@ def test_nan_alpha_follows_each_reference_path(ctx, orc):
     gl, gg = ctx.fused_loss_backward(params, target, 0.01)  # grad.rs:61-62 culls it
     cl, cg = orc.loss_backward_batch(params, target, 0.01)
     check_losses(gl, cl)
-    assert grad_err(gg, cg) <= GRAD_RTOL and np.all(gg[0, 2] == 0)
+    assert_grads(gg, cg)
+    assert np.all(gg[0, 2] == 0)
 
 
 def test_empty_scene_and_empty_batch(ctx, orc):
@@ -238,7 +202,7 @@ def test_results_are_bit_reproducible(ctx, orc):
     assert grad_err(c[1], a[1]) <= 1e-6
     cl, cg = orc.loss_backward_batch(params, targets, 0.0015)
     check_losses(a[0], cl)
-    assert grad_err(a[1], cg) <= GRAD_RTOL
+    assert_grads(a[1], cg)
     gin = ((synth.uniforms(6, 4 * 96 * 96 * 3) - 0.5) * 1e-3).reshape(4, 96, 96, 3).astype(np.float32)
     d1 = ctx.backward_from_grad(params, gin, 0.0015, deterministic=True)
     d2 = ctx.backward_from_grad(params, gin, 0.0015, deterministic=True)
@@ -315,9 +279,20 @@ def test_device_fit_tracks_the_oracle(ctx, orc):  # fit.rs:166-288
     c = orc.fit(target, init, bg, iters=60, patience=None)
     assert g["stop_reason"] == c["stop_reason"] == "Completed"
     assert len(g["losses"]) == len(c["losses"]) == 60
-    assert abs(g["losses"][0] - c["losses"][0]) <= 1e-5 * c["losses"][0]
-    assert np.all(np.abs(g["losses"] - c["losses"]) <= 2e-2 * c["losses"])
+    rel = np.abs(g["losses"] - c["losses"]) / c["losses"]
+    print(f"fit 40x40 T=12: loss rel err first 20 {rel[:20].max():.2e}, all 60 {rel.max():.2e}; "
+          f"best iter gpu {g['best_iter']} oracle {c['best_iter']}", flush=True)
+    assert rel[:20].max() <= 1e-4
+    assert rel.max() <= 1e-3
     assert g["best_loss"] == g["losses"][g["best_iter"]]
+    # the snapshot is the scene the best loss was measured on (taken before the update)
+    sig = orc.sigma_at(0.02, 0.0015, 60, g["best_iter"])
+    again = orc.mse(orc.render(g["best_params"], 40, 40, sig, bg), target)
+    assert abs(again - g["best_loss"]) <= 1e-4 * g["best_loss"]
+    if g["best_iter"] == c["best_iter"]:
+        d = np.abs(g["best_params"] - c["best_params"]).max()
+        print(f"fit 40x40 T=12: best params max abs diff {d:.2e}", flush=True)
+        assert d <= 1e-3
 
 
 def test_device_fit_stop_reasons(ctx):
@@ -346,10 +321,10 @@ def test_rebuild_path_past_the_recorded_entries(ctx, orc, monkeypatch):
         for det in (False, True):
             l, g = ctx.fused_loss_backward(params, targets, 0.004, bgs, deterministic=det)
             check_losses(l, want_l)
-            assert grad_err(g, want_g) <= GRAD_RTOL
+            assert_grads(g, want_g, label=f"rebuild cap={cap} det={det}")
         gi = np.random.default_rng(1).standard_normal((2, 40, 48, 3)).astype(np.float32) * 1e-3
         g2 = ctx.backward_from_grad(params, gi, 0.004, bgs)
-        assert grad_err(g2, orc.backward_from_grad_batch(params, gi, 0.004, bgs)) <= GRAD_RTOL
+        assert_grads(g2, orc.backward_from_grad_batch(params, gi, 0.004, bgs))
 
 
 def test_channels_first_layout_gives_the_same_numbers(ctx):

@@ -16,6 +16,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from bars import assert_grads
 from diffrast.torch_layer import (
     N_PARAMS,
     clamp_params,
@@ -121,8 +122,7 @@ def test_rasterize_routes_to_the_gpu(orc):  # test_torch_layer.py:126-144
     out.sum().backward()
     assert last_device() == "gpu"
     ref = orc.backward_from_grad_batch(p.detach().numpy(), np.ones((8, 64, 64, 3), np.float32), 0.02)
-    rel = np.abs(p.grad.numpy() - ref).max() / max(np.linalg.norm(ref), 1e-12)
-    assert rel < 1e-2, f"gpu/oracle gradient gap {rel:.2e}"
+    assert_grads(p.grad.numpy(), ref, label="rasterize backward")
 
 
 def test_cpu_device_is_rejected():
@@ -166,7 +166,7 @@ def test_fused_loss_matches_autograd_path():  # test_torch_layer.py:165-179
     per_item = ((rendered - targets) ** 2).flatten(1).mean(1)
     per_item.sum().backward()
     torch.testing.assert_close(losses, per_item.detach(), rtol=1e-4, atol=1e-6)
-    torch.testing.assert_close(grads, pg.grad, rtol=1e-3, atol=1e-7)
+    assert_grads(grads.numpy(), pg.grad.numpy(), label="fused vs autograd")
 
 
 @gpu
@@ -187,8 +187,7 @@ def test_gpu_gradients_agree_with_the_oracle(orc):  # test_torch_layer.py:200-21
     gpu_loss, gpu_grads = fused_loss(p, targets, sigma=0.02)
     cpu_loss, cpu_grads = orc.loss_backward_batch(p.numpy(), targets.numpy(), 0.02)
     torch.testing.assert_close(gpu_loss, torch.from_numpy(cpu_loss), rtol=1e-4, atol=1e-7)
-    rel = np.abs(gpu_grads.numpy() - cpu_grads).max() / max(np.linalg.norm(cpu_grads), 1e-12)
-    assert rel < 1e-3, f"relative gradient difference {rel:.2e}"
+    assert_grads(gpu_grads.numpy(), cpu_grads, label="fused_loss")
     # bit-identical would mean the GPU path did not run
     assert not np.array_equal(gpu_grads.numpy(), cpu_grads)
 
