@@ -219,4 +219,9 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
                int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
                hipStream_t s, const int* halt = nullptr);
 
+// Called by drh_create with the context's device current: takes the device
+// address of the scratch array of drh_fused_loss_backward_noalloc on that
+// device (once per device).
+int scratch_init(int device);
+
 }  // namespace drh_rt

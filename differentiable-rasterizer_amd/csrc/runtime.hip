@@ -534,6 +534,11 @@ int drh_create(drh_ctx** out) {
     char buf[512];
     std::snprintf(buf, sizeof buf, "%s (%s, %d CUs, HIP)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
     c->info = buf;
+    int rc = scratch_init(dev);
+    if (rc) {
+        delete c;
+        return rc;
+    }
     *out = c;
     return DRH_OK;
 }

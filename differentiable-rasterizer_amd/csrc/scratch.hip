@@ -1,0 +1,136 @@
+// drh_fused_loss_backward_noalloc: drh_fused_loss_backward for callers that
+// cannot allocate device memory (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc). Its buffers besides the caller's
+// inputs and outputs (triangle records, per-pixel hand-over, per-tile entry
+// lists, loss partials, block order, and with DRH_DETERMINISTIC the partial
+// gradient rows) live in one file-scope device array of SCRATCH_BYTES, which
+// every GPU the library runs on holds until the process ends. The entry point
+// calls no hipMalloc, hipFree or other allocating routine.
+//
+// In host code `scratch` is a host-side stand-in for the array, not a device
+// address: scratch_init takes the device address once per device (with that
+// device current) and only that address is used afterwards. Every call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU race.
+
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "runtime.h"
+
+using drh::NP;
+using namespace drh_rt;
+
+constexpr size_t SCRATCH_BYTES = 128ull << 20;  // 128 MiB per GPU
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_mu;
+std::vector<void*> g_addr;  // device address of `scratch`, per device
+
+void* scratch_addr(int device) {
+    std::lock_guard<std::mutex> g(g_mu);
+    return device >= 0 && (size_t)device < g_addr.size() ? g_addr[device] : nullptr;
+}
+
+// Offsets of the buffers of one call in the scratch array, each at a 256-byte
+// boundary; the tile-entry lists take what the rest leaves (all T entries per
+// tile when they fit, else fewer, and tiles past them rebuild their lists in
+// the backward kernel).
+struct ScratchLayout {
+    size_t rec = 0, ploss = 0, pstate = 0, tn = 0, order = 0, partials = 0, tent = 0, total = 0;
+    int cap2 = 0;
+    bool ordered = false;
+};
+
+ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, bool det) {
+    ScratchLayout L;
+    const dim3 grid = drh::raster_grid(B, W, H);
+    const size_t nblk = (size_t)grid.x * grid.y, ntiles = (size_t)B * nblk * drh::WAVES;
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t off = 0;
+    L.rec = off;
+    off = up(off + (size_t)B * T * drh::REC * sizeof(float));
+    L.ploss = off;
+    off = up(off + (size_t)B * nblk * sizeof(double));
+    L.pstate = off;
+    off = up(off + (size_t)B * H * W * sizeof(drh::PixState));
+    L.tn = off;
+    off = up(off + ntiles * 2 * sizeof(int));
+    L.ordered = use_order(ctx, B, (int)grid.x, (int)grid.y);
+    L.order = off;
+    if (L.ordered) off = up(off + (size_t)B * nblk * sizeof(int));
+    L.partials = off;
+    if (det) off = up(off + (size_t)B * nblk * T * NP * sizeof(float));
+    L.tent = off;
+    const size_t left = SCRATCH_BYTES > off ? SCRATCH_BYTES - off : 0;
+    L.cap2 = tile_entries(ntiles, T, left, 1);
+    L.total = up(off + ntiles * (size_t)L.cap2 * sizeof(drh::TileEnt));
+    return L;
+}
+
+}  // namespace
+
+namespace drh_rt {
+
+int scratch_init(int device) {
+    std::lock_guard<std::mutex> g(g_mu);
+    if ((size_t)device >= g_addr.size()) g_addr.resize((size_t)device + 1, nullptr);
+    if (g_addr[device]) return DRH_OK;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_addr[device] = p;
+    return DRH_OK;
+}
+
+}  // namespace drh_rt
+
+extern "C" {
+
+int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const float* backgrounds,
+                                    const float* targets, int64_t B, int64_t T, int64_t H, int64_t W, float sigma,
+                                    float* out_losses, float* out_grads, float* out_images, void* stream,
+                                    uint32_t flags) {
+    int rc = check_shape(ctx, B, T, H, W, sigma);
+    if (rc) return rc;
+    if (flags & DRH_HOST_PTRS)
+        return fail(DRH_ERR_INVALID_ARG, "drh_fused_loss_backward_noalloc takes device pointers only "
+                                         "(host arrays would need staging buffers)");
+    if (B == 0) return DRH_OK;
+    if (!params && T > 0) return fail(DRH_ERR_INVALID_ARG, "input pointer is NULL");
+    if (!targets || !out_losses || !backgrounds || (T > 0 && !out_grads))
+        return fail(DRH_ERR_INVALID_ARG, "output, target or background pointer is NULL");
+    const bool det = (flags & DRH_DETERMINISTIC) != 0;
+    const ScratchLayout L = scratch_layout(ctx, (int)B, (int)T, (int)H, (int)W, det);
+    if (L.total > SCRATCH_BYTES)
+        return fail(DRH_ERR_TOO_LARGE, "these sizes need " + std::to_string(L.total) + " bytes of scratch; the " +
+                                           "entry point that allocates nothing has " +
+                                           std::to_string(SCRATCH_BYTES) + " (use drh_fused_loss_backward)");
+    DeviceGuard dg(ctx->device);
+    char* base = static_cast<char*>(scratch_addr(ctx->device));
+    if (!base) return fail(DRH_ERR_DEVICE, "scratch array not initialised on this device");
+    RasterBufs bufs;
+    bufs.rec = reinterpret_cast<float*>(base + L.rec);
+    bufs.ploss = reinterpret_cast<double*>(base + L.ploss);
+    bufs.pstate = reinterpret_cast<drh::PixState*>(base + L.pstate);
+    bufs.tn = reinterpret_cast<int*>(base + L.tn);
+    bufs.order = L.ordered ? reinterpret_cast<int*>(base + L.order) : nullptr;
+    bufs.partials = det ? reinterpret_cast<float*>(base + L.partials) : nullptr;
+    bufs.tent = reinterpret_cast<drh::TileEnt*>(base + L.tent);
+    bufs.cap2 = L.cap2;
+    // Nothing in the scratch array needs to start at zero: every buffer is
+    // written by this call's kernels before it is read (the gradients are the
+    // caller's output and setup_records clears them).
+    hipStream_t s = (hipStream_t)stream;
+    if ((rc = run_raster_bufs(ctx, drh::MODE_LOSS, params, backgrounds, targets, (int)B, (int)T, (int)H, (int)W,
+                              sigma, out_images, out_grads, out_losses, flags, bufs, s, nullptr, false)))
+        return rc;
+    if (flags & DRH_SYNC) HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return DRH_OK;
+}
+
+}  // extern "C"

@@ -117,6 +117,8 @@ SIGNATURES = {
     "drh_render": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _U32], ctypes.c_int),
     "drh_fused_loss_backward": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _U32],
                                 ctypes.c_int),
+    "drh_fused_loss_backward_noalloc": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _U32],
+                                        ctypes.c_int),
     "drh_backward_from_grad": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _U32], ctypes.c_int),
     "drh_adam_project_step": ([_P, _P, _P, _P, _P, _P, _I64, _U32, _F32, _F32, _F32, ctypes.c_int, _P, _U32],
                               ctypes.c_int),
@@ -259,6 +261,12 @@ class Context:
                   stream=None, flags=0):
         check(lib().drh_fused_loss_backward(self.handle, params, bgs, targets, B, T, H, W, sigma,
                                             losses, grads, images, stream, flags))
+
+    def fused_noalloc_ptr(self, params, bgs, targets, B, T, H, W, sigma, losses, grads, images=None,
+                          stream=None, flags=0):
+        """drh_fused_loss_backward_noalloc: device pointers, no device allocation."""
+        check(lib().drh_fused_loss_backward_noalloc(self.handle, params, bgs, targets, B, T, H, W, sigma,
+                                                    losses, grads, images, stream, flags))
 
     def from_grad_ptr(self, params, bgs, grad_images, B, T, H, W, sigma, grads, stream=None, flags=0):
         check(lib().drh_backward_from_grad(self.handle, params, bgs, grad_images, B, T, H, W, sigma,

@@ -115,6 +115,21 @@ int drh_fused_loss_backward(drh_ctx *ctx, const float *params, const float *back
                             float sigma, float *out_losses, float *out_grads, float *out_images,
                             void *stream, uint32_t flags);
 
+/* drh_fused_loss_backward for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Device pointers only
+ * (DRH_HOST_PTRS is refused: staging would allocate). The call's buffers
+ * besides its inputs and outputs live in a 128 MiB array that the library
+ * holds on each GPU until the process ends; sizes whose buffers exceed it
+ * (far beyond B=16 at 256x256, T=128) return DRH_ERR_TOO_LARGE. Calls that
+ * overlap on one GPU share that array and race: the caller orders them (one
+ * stream, or events). Results equal drh_fused_loss_backward's; its
+ * launches are not counted by drh_timing_*. */
+int drh_fused_loss_backward_noalloc(drh_ctx *ctx, const float *params, const float *backgrounds,
+                                    const float *targets, int64_t B, int64_t T, int64_t H, int64_t W,
+                                    float sigma, float *out_losses, float *out_grads, float *out_images,
+                                    void *stream, uint32_t flags);
+
 /* Parameter gradients from an upstream image gradient dL/dpixel
  * (B x H x W x 3): backward_many_from_grad
  * (crates/diffrast-gpu/src/lib.rs:828-910) and backward_batch

@@ -1,0 +1,93 @@
+"""drh_fused_loss_backward_noalloc: the fused entry point whose buffers live in
+the library's fixed scratch array instead of the pool. Its results must equal
+drh_fused_loss_backward's: bit for bit with fixed-order sums, to 1e-6 of the
+gradient norm with the default float atomics (their order varies run to run)."""
+
+import numpy as np
+import pytest
+
+from bars import assert_grads, check_losses
+from diffrast import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+SIGMA = 0.0015
+
+
+def run_both(ctx, torch, dev, B, H, W, T, kind, seed, flags):
+    s = torch.cuda.current_stream(dev).cuda_stream
+    params = torch.from_numpy(synth.batch(kind, B, T, seed)).to(dev)
+    tp = torch.from_numpy(synth.batch(kind, B, T, seed, target_offset=1000)).to(dev)
+    bg = torch.zeros((B, 3), device=dev)
+    targets = torch.empty((B, H, W, 3), device=dev)
+    ctx.render_ptr(tp.data_ptr(), bg.data_ptr(), B, T, H, W, SIGMA, targets.data_ptr(), s)
+    out = {}
+    for name in ("pooled", "noalloc"):
+        losses = torch.full((B,), float("nan"), device=dev)
+        grads = torch.full((B, T, 10), float("nan"), device=dev)
+        images = torch.full((B, H, W, 3), float("nan"), device=dev)
+        fn = ctx.fused_ptr if name == "pooled" else ctx.fused_noalloc_ptr
+        fn(params.data_ptr(), bg.data_ptr(), targets.data_ptr(), B, T, H, W, SIGMA, losses.data_ptr(),
+           grads.data_ptr(), images.data_ptr(), s, flags)
+        out[name] = (losses, grads, images)
+    torch.cuda.synchronize()
+    return out, params, targets
+
+
+@pytest.mark.parametrize("flags", [_lib.DETERMINISTIC, 0], ids=["fixed-order", "atomic"])
+def test_noalloc_matches_the_pooled_entry_point(flags):
+    import torch
+
+    dev = torch.device("cuda:0")
+    ctx = _lib.Context()
+    # two calls in a row, the second smaller (and with T > 128: several triangle chunks)
+    for B, H, W, T, kind in [(16, 256, 256, 128, "uniform"), (3, 40, 56, 300, "small")]:
+        print(f"noalloc B={B} {H}x{W} T={T} flags={flags}", flush=True)
+        before = ctx.pool_stats()
+        out, params, targets = run_both(ctx, torch, dev, B, H, W, T, kind, 7, flags)
+        (lp, gp, ip), (ln, gn, inn) = out["pooled"], out["noalloc"]
+        assert torch.equal(ip, inn)
+        assert torch.equal(lp, ln)  # the losses are summed in a fixed order either way
+        if flags & _lib.DETERMINISTIC:
+            assert torch.equal(gp, gn)
+        else:
+            assert_grads(gn.cpu().numpy(), gp.cpu().numpy(), tol=1e-6, label="noalloc vs pooled")
+        after = ctx.pool_stats()
+        # the pooled call borrowed its buffers from the pool; the noalloc call took none
+        assert after["misses"] - before["misses"] <= 7
+    # the smaller call's results also meet the oracle bars
+    from oracle import oracle as orc
+
+    cl, cg = orc.loss_backward_batch(params.cpu().numpy(), targets.cpu().numpy(), SIGMA)
+    check_losses(ln.cpu().numpy(), cl)
+    assert_grads(gn.cpu().numpy(), cg)
+    ctx.close()
+
+
+def test_noalloc_takes_no_pool_buffer_and_refuses_what_it_cannot_do():
+    import torch
+
+    dev = torch.device("cuda:0")
+    ctx = _lib.Context()
+    s = torch.cuda.current_stream(dev).cuda_stream
+    B, H, W, T = 2, 32, 32, 20
+    p = torch.from_numpy(synth.batch("uniform", B, T, 3)).to(dev)
+    bg = torch.zeros((B, 3), device=dev)
+    tg = torch.rand((B, H, W, 3), device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+    losses, grads = torch.empty(B, device=dev), torch.empty((B, T, 10), device=dev)
+    ctx.fused_noalloc_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), B, T, H, W, SIGMA, losses.data_ptr(),
+                          grads.data_ptr(), None, s, _lib.SYNC)
+    st = ctx.pool_stats()
+    assert st["hits"] == 0 and st["misses"] == 0 and st["bytes"] == 0
+    assert torch.isfinite(losses).all() and torch.isfinite(grads).all()
+    # host arrays would need staging buffers
+    with pytest.raises(_lib.DiffrastError) as e:
+        ctx.fused_noalloc_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), B, T, H, W, SIGMA, losses.data_ptr(),
+                              grads.data_ptr(), None, s, _lib.HOST_PTRS)
+    assert e.value.code == 6
+    # sizes whose buffers exceed the scratch array are refused before any launch
+    with pytest.raises(_lib.DiffrastError) as e:
+        ctx.fused_noalloc_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), 16, T, 1024, 1024, SIGMA,
+                              losses.data_ptr(), grads.data_ptr(), None, s, 0)
+    assert e.value.code == 5 and "scratch" in str(e.value)
+    ctx.close()
