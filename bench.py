@@ -12,10 +12,14 @@ evaluations per second, ms per batch, the dominant kernel's roofline position
 (backward_kernel: its algorithmic FLOP per launch over its event-timed average
 duration, against the FP32 vector peak; the forward kernel and the pair are
 reported beside it), the CPU baseline (the C oracle, one thread per scene, on
-this host's cores), and side measurements of the other workloads.
+this host's cores), and under "configs" the same measurements for every
+benchmark workload: c0 (B=1 64x64 T=32), c1 (B=16 128x128 T=128), c2 (the
+headline), c3 (B=8 256x256 T=512 small triangles) and c4 (the 800-iteration
+fit at 176x176, T=150, against the oracle's fit on one core).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
     python bench.py --copy-calibration     # plain device copy, for PMC scaling
+    python bench.py --crossover            # GPU vs this host's CPU over the reference's crossover cells
 """
 
 from __future__ import annotations
@@ -49,6 +53,8 @@ SIGMA = 0.0015                # python/diffrast/torch_layer.py:73
 # forward_kernel: 74 box + 10 contrib + 15 pixel; backward_kernel: 74 box + 51 contrib
 FLOP_FWD = (74, 10, 15)
 FLOP_BWD = (74, 51, 0)
+# parameter groups of the per-group gradient parity figures
+GROUPS = {"vertices": slice(0, 6), "colours": slice(6, 9), "alpha": slice(9, 10)}
 
 
 def log(*a):
@@ -121,42 +127,81 @@ def traffic_from_profiles(kernel):
     return float(m.group(1)) if m else None
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def timed_reps(fn, warmup=3, budget_s=0.4, min_reps=3, max_reps=50):
+    """benches/raster.rs:22-40 protocol: `warmup` untimed runs, then timed runs until
+    `budget_s` seconds and `min_reps` runs have passed; returns the per-run seconds."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    while (sum(times) < budget_s or len(times) < min_reps) and len(times) < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
 def cpu_baseline(cfg, params, targets_np, budget_s):
-    """The oracle's backward_batch analogue on this host (grad.rs:192-207)."""
+    """The oracle's backward_batch analogue on this host (grad.rs:192-207): one thread
+    per scene as rayon's par_iter, capped by the cores this process may use (16 per
+    GPU on a shared box, whatever the machine's total); and one item on one thread."""
     from oracle import oracle
 
-    B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
-    # one thread per scene, capped by the cores this process may use (16 per
-    # GPU on a shared box, whatever the machine's total)
+    B = cfg["B"]
     threads = max(1, min(B, box_cpu_share(), 16))
     counts = oracle.Counts()
-    t0 = time.perf_counter()
-    losses, grads = oracle.loss_backward_batch(params, targets_np, SIGMA, nthreads=threads,
-                                               counts=counts)
-    first = time.perf_counter() - t0
-    reps, t_total = 0, 0.0
-    while t_total < budget_s and reps < 50:
-        t0 = time.perf_counter()
-        oracle.loss_backward_batch(params, targets_np, SIGMA, nthreads=threads)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    per_batch = t_total / reps if reps else first
-    return dict(per_batch_s=per_batch, reps=reps, threads=threads, losses=losses, grads=grads,
+    losses, grads = oracle.loss_backward_batch(params, targets_np, SIGMA, nthreads=threads, counts=counts)
+    times = timed_reps(lambda: oracle.loss_backward_batch(params, targets_np, SIGMA, nthreads=threads),
+                       warmup=2, budget_s=budget_s)  # the counted run above is the first warm-up
+    single = timed_reps(lambda: oracle.loss_backward_batch(params[:1], targets_np[:1], SIGMA, nthreads=1),
+                        warmup=1, budget_s=min(budget_s, 0.4), min_reps=2)
+    return dict(per_batch_s=float(np.mean(times)), median_s=float(np.median(times)), reps=len(times),
+                threads=threads, single_item_ms=float(np.median(single)) * 1e3, losses=losses, grads=grads,
                 n_box=int(counts.n_box), n_contrib=int(counts.n_contrib))
 
 
-def fit_side(ctx):
-    """Config c4: the device fit loop, 800 iterations at 176x176, T=150."""
+def fit_config(ctx, with_cpu=True):
+    """Config c4: the device fit loop, 800 iterations at 176x176, T=150, against the
+    oracle's fit of the same start on one core (fit.rs:243-288 is sequential)."""
     from diffrast import synth
 
-    target = synth.blob_target(4, 176, 176)
-    init, bg = synth.seed_scene(target, 150, 4)
+    cfg = synth.CONFIGS["c4"]
+    H, W, T, iters = cfg["H"], cfg["W"], cfg["T"], cfg["iters"]
+    target = synth.blob_target(4, H, W)
+    init, bg = synth.seed_scene(target, T, 4)
     ctx.fit(target, init, bg, iters=20, patience=None)  # warm-up
-    t0 = time.perf_counter()
-    r = ctx.fit(target, init, bg, iters=800, patience=None)
-    dt = time.perf_counter() - t0
-    return dict(seconds=round(dt, 4), iterations=len(r["losses"]), first_loss=float(r["losses"][0]),
-                best_loss=r["best_loss"], improvement=float(r["losses"][0] / r["best_loss"]))
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        r = ctx.fit(target, init, bg, iters=iters, patience=None)
+        runs.append(time.perf_counter() - t0)
+    dt = float(np.median(runs))
+    out = dict(workload=f"device fit loop, B=1 {H}x{W} T={T}, {iters} iterations (patience off), "
+                        "sigma 0.02 -> 0.0015, Adam lr 0.004/0.02/0.01",
+               iterations=len(r["losses"]), seconds=round(dt, 4), ms_per_iteration=dt * 1e3 / iters,
+               first_loss=float(r["losses"][0]), best_loss=r["best_loss"], best_iter=r["best_iter"],
+               improvement=float(r["losses"][0] / r["best_loss"]))
+    if with_cpu:
+        from oracle import oracle
+
+        t0 = time.perf_counter()
+        c = oracle.fit(target, init, bg, iters=iters, patience=None)
+        cpu_s = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": iters / cpu_s, "unit": "iterations/s", "cores": 1, "kind": "port",
+                               "sample": f"the whole {iters}-iteration fit once, one thread",
+                               "seconds": round(cpu_s, 3), "ms_per_iteration": cpu_s * 1e3 / iters,
+                               "best_loss": c["best_loss"], "best_iter": c["best_iter"]}
+        out["speedup_gpu_over_cpu"] = cpu_s / dt
+    return out
 
 
 def torch_op_ms(torch, cfg, p, targets, dev, steps=10):
@@ -270,15 +315,136 @@ def copy_calibration(torch):
     print(json.dumps({"copy_bytes_each_way": n * 4}), flush=True)
 
 
+def roof(kernel, flop, ms_k, traffic=None):
+    achieved = flop / (ms_k / 1e3) / 1e12
+    return {
+        "bound": "valu",
+        "achieved": achieved,
+        "peak": PEAK_FP32_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": achieved / PEAK_FP32_TFLOPS,
+        "traffic": traffic,
+        "kernel": kernel,
+        "flop_per_launch": flop,
+        "ms_per_launch": ms_k,
+    }
+
+
+def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic=False):
+    """One batched workload: wall ms per fused step, per-kernel event times, and (with
+    `cpu`) the oracle's counts, parity, rooflines and the same-run CPU baseline."""
+    from diffrast import synth
+
+    cfg = synth.CONFIGS[name]
+    B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
+    params, p, bg, targets = make_inputs(torch, ctx, cfg, 1, dev)
+    ms, losses, grads = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)
+    kt = kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(steps, 50)), dev)
+    log(f"{name}: {ms:.4f} ms/batch over {steps} steps; kernel avg ms {kt}")
+    dense = B * H * W * T
+    out = {
+        "workload": f"batched soft-raster forward+MSE+backward, B={B} {H}x{W} T={T} sigma={SIGMA}"
+                    + (" (small triangles)" if cfg["kind"] == "small" else ""),
+        "B": B, "H": H, "W": W, "T": T,
+        "ms_per_batch": ms,
+        "pixel_tri_per_s": dense / (ms / 1e3),
+        "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
+    }
+    if not cpu:
+        return out
+    targets_np = targets.cpu().numpy()
+    c = cpu_baseline(cfg, params, targets_np, cpu_budget)
+    log(f"{name}: cpu baseline {c['per_batch_s'] * 1e3:.1f} ms/batch on {c['threads']} threads")
+    g = grads.cpu().numpy().reshape(B, -1, 10).astype(np.float64)
+    cg = c["grads"].reshape(B, -1, 10).astype(np.float64)
+    par = {"grad_max_abs_over_norm": max(float(np.abs(g[b] - cg[b]).max() / np.linalg.norm(cg[b]))
+                                         for b in range(B))}
+    for gname, sl in GROUPS.items():
+        par[f"grad_{gname}"] = max(float(np.abs(g[b][:, sl] - cg[b][:, sl]).max() /
+                                         max(np.linalg.norm(cg[b][:, sl]), 1e-30)) for b in range(B))
+    l = losses.cpu().numpy().astype(np.float64)
+    par["loss_rel"] = float(np.max(np.abs(l - c["losses"]) / np.abs(c["losses"])))
+    out["parity_vs_oracle"] = par
+    counts = (c["n_box"], c["n_contrib"], B * H * W)
+    flop_f = sum(a * b for a, b in zip(FLOP_FWD, counts))
+    flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
+    out["roofline"] = roof("backward_kernel", flop_b, kt["backward"],
+                           traffic_from_profiles("backward_kernel") if traffic else None)
+    out["roofline"]["n_box_pairs"] = c["n_box"]
+    out["roofline"]["n_contrib_pairs"] = c["n_contrib"]
+    out["roofline_forward"] = roof("forward_kernel", flop_f, kt["forward"],
+                                   traffic_from_profiles("forward_kernel") if traffic else None)
+    out["roofline_pair"] = roof("forward_kernel+backward_kernel", flop_f + flop_b, kt["forward"] + kt["backward"])
+    out["roofline_step"] = roof("whole step (wall)", flop_f + flop_b, ms)
+    out["cpu_baseline"] = {
+        "value": dense / c["per_batch_s"],
+        "unit": UNIT,
+        "cores": c["threads"],
+        "kind": "port",
+        "sample": f"the full B={B} {H}x{W} T={T} batch: 3 warm-ups, then {c['reps']} timed runs "
+                  f"(>= 0.4 s), one thread per scene",
+        "ms_per_batch": c["per_batch_s"] * 1e3,
+        "median_ms_per_batch": c["median_s"] * 1e3,
+        "single_thread_ms_per_item": c["single_item_ms"],
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
+        "threads": c["threads"],
+        "speedup_gpu_over_cpu": c["per_batch_s"] * 1e3 / ms,
+    }
+    return out
+
+
+def crossover(torch, ctx, dev):
+    """GPU against this host's CPU over the reference's crossover cells (batch of 16,
+    64/128/256 pixels, 32/128/512 triangles, sigma 0.01, Scene::random-shaped scenes,
+    flat targets; crates/diffrast-gpu/src/bin/gpu_bench.rs:157-182) and small cells
+    near the reference's dispatch floor (crates/diffrast-py/src/lib.rs:138-147). The
+    GPU is timed with host arrays in and out, as the reference's backward_many takes
+    them, and with device-resident arrays."""
+    from diffrast import synth
+    from oracle import oracle
+
+    cells = [(16, n, t) for n in (64, 128, 256) for t in (32, 128, 512)]
+    cells += [(1, 16, 2), (1, 32, 8), (2, 32, 16), (1, 64, 32), (2, 64, 32), (4, 64, 64), (1, 128, 64)]
+    rows = []
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for B, n, T in cells:
+        params = np.stack([synth.random_scene(11 + b, T) for b in range(B)])
+        targets = np.empty((B, n, n, 3), np.float32)
+        targets[:] = (0.4, 0.5, 0.6)
+        threads = max(1, min(B, box_cpu_share(), 16))
+        cpu = np.median(timed_reps(lambda: oracle.loss_backward_batch(params, targets, 0.01, nthreads=threads),
+                                   warmup=1, budget_s=0.2))
+        host = np.median(timed_reps(lambda: ctx.fused_loss_backward(params, targets, 0.01), warmup=2,
+                                    budget_s=0.1, min_reps=5))
+        p, tg = torch.from_numpy(params).to(dev), torch.from_numpy(targets).to(dev)
+        bg = torch.zeros((B, 3), device=dev)
+        l, g = torch.empty(B, device=dev), torch.empty((B, T, 10), device=dev)
+
+        def dev_step():
+            ctx.fused_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), B, T, n, n, 0.01, l.data_ptr(), g.data_ptr(),
+                          None, stream)
+            torch.cuda.synchronize()
+
+        devt = np.median(timed_reps(dev_step, warmup=2, budget_s=0.1, min_reps=5))
+        rows.append(dict(batch=B, size=n, tris=T, work=B * T * n * n, cpu_ms=cpu * 1e3, cpu_threads=threads,
+                         gpu_host_ms=host * 1e3, gpu_device_ms=devt * 1e3, gpu_host_over_cpu=cpu / host,
+                         reference_rule_prefers_gpu=bool(B >= 2 and B * T * n * n >= 250_000)))
+        log(json.dumps(rows[-1]))
+    print(json.dumps({"crossover": rows, "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+                      "device": ctx.device_info()}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds of CPU baseline timing")
+    ap.add_argument("--cpu-budget", type=float, default=0.4, help="seconds of timed CPU baseline runs per config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-side", action="store_true", help="skip the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--crossover", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -298,15 +464,14 @@ def main():
     torch.cuda.set_device(dev)
     ctx = _lib.Context()
     log("device:", ctx.device_info())
+    if args.crossover:
+        crossover(torch, ctx, dev)
+        return
     cfg = synth.CONFIGS["c2"]
     B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
-
-    params, p, bg, targets = make_inputs(torch, ctx, cfg, 1, dev)
-    ms, losses, grads = time_fused(torch, ctx, cfg, p, bg, targets, args.steps, args.warmup, dev)
-    log(f"c2: {ms:.4f} ms/batch over {args.steps} steps")
-    kt = kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(args.steps, 50)), dev)
-    log("kernel avg ms:", kt)
-
+    cpu = not args.no_cpu_baseline
+    head = measure_batch(torch, ctx, "c2", dev, args.steps, args.warmup, cpu, args.cpu_budget, traffic=True)
+    ms = head["ms_per_batch"]
     dense = B * H * W * T
     out = {
         "metric": METRIC,
@@ -321,76 +486,32 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded SplitMix64 scenes; targets rendered from independently seeded scenes)",
-        "config": {"workload": "batched soft-raster forward+MSE+backward, B=16 256x256 T=128 sigma=0.0015",
-                   "B": B, "H": H, "W": W, "T": T, "sigma": SIGMA, "scenes": "uniform vertices"},
-        "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
+        "config": {"workload": head["workload"], "B": B, "H": H, "W": W, "T": T, "sigma": SIGMA,
+                   "scenes": "uniform vertices"},
+        "kernel_ms": head["kernel_ms"],
+        "parity_vs_oracle": head.get("parity_vs_oracle"),
+        "roofline": head.get("roofline"),
+        "roofline_forward": head.get("roofline_forward"),
+        "roofline_pair": head.get("roofline_pair"),
+        "roofline_step": head.get("roofline_step"),
+        "cpu_baseline": head.get("cpu_baseline"),
     }
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        targets_np = targets.cpu().numpy()
-        cpu = cpu_baseline(cfg, params, targets_np, args.cpu_budget)
-        log(f"cpu baseline: {cpu['per_batch_s'] * 1e3:.1f} ms/batch on {cpu['threads']} threads")
-        g = grads.cpu().numpy().reshape(B, -1).astype(np.float64)
-        cg = cpu["grads"].reshape(B, -1).astype(np.float64)
-        grad_rel = max(float(np.abs(g[b] - cg[b]).max() / np.linalg.norm(cg[b])) for b in range(B))
-        l = losses.cpu().numpy().astype(np.float64)
-        loss_rel = float(np.max(np.abs(l - cpu["losses"]) / np.abs(cpu["losses"])))
-        out["parity_vs_oracle"] = {"grad_max_abs_over_norm": grad_rel, "loss_rel": loss_rel}
-        counts = (cpu["n_box"], cpu["n_contrib"], B * H * W)
-        flop_f = sum(a * b for a, b in zip(FLOP_FWD, counts))
-        flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
-
-        def roof(kernel, flop, ms_k):
-            achieved = flop / (ms_k / 1e3) / 1e12
-            return {
-                "bound": "valu",
-                "achieved": achieved,
-                "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s",
-                "frac": achieved / PEAK_FP32_TFLOPS,
-                "traffic": traffic_from_profiles(kernel),
-                "kernel": kernel,
-                "flop_per_launch": flop,
-                "ms_per_launch": ms_k,
-            }
-
-        out["roofline"] = roof("backward_kernel", flop_b, kt["backward"])
-        out["roofline"]["n_box_pairs"] = cpu["n_box"]
-        out["roofline"]["n_contrib_pairs"] = cpu["n_contrib"]
-        out["roofline_forward"] = roof("forward_kernel", flop_f, kt["forward"])
-        both = roof("forward_kernel+backward_kernel", flop_f + flop_b, kt["forward"] + kt["backward"])
-        both["traffic"] = None
-        out["roofline_pair"] = both
-        out["cpu_baseline"] = {
-            "value": dense / cpu["per_batch_s"],
-            "unit": UNIT,
-            "cores": cpu["threads"],
-            "kind": "port",
-            "sample": f"the full B=16 256x256 T=128 batch, {cpu['reps']} timed repetitions "
-                      f"({cpu['per_batch_s'] * 1e3:.1f} ms each) after one untimed run, "
-                      "one thread per scene",
-            "ms_per_batch": cpu["per_batch_s"] * 1e3,
-            "speedup_gpu_over_cpu": cpu["per_batch_s"] * 1e3 / ms,
-        }
-    else:
-        out["roofline"] = None
-        out["cpu_baseline"] = None
-
     if not args.no_side:
+        configs = {}
+        for name in ("c0", "c1"):
+            configs[name] = measure_batch(torch, ctx, name, dev, 20, 5, cpu, args.cpu_budget)
+        configs["c2"] = head
+        configs["c3"] = measure_batch(torch, ctx, "c3", dev, 20, 5, cpu, args.cpu_budget)
+        configs["c4"] = fit_config(ctx, with_cpu=cpu)
+        out["configs"] = configs
+        p = torch.from_numpy(synth.batch("uniform", B, T, 1)).to(dev)
+        _, _, _, targets = make_inputs(torch, ctx, cfg, 1, dev)
         side = {}
-        for name in ("c0", "c1", "c3"):
-            c = synth.CONFIGS[name]
-            _, pp, bb, tt = make_inputs(torch, ctx, c, 1, dev)
-            m, _, _ = time_fused(torch, ctx, c, pp, bb, tt, 20, 5, dev)
-            side[name] = {"ms_per_batch": round(m, 4), "B": c["B"], "H": c["H"], "W": c["W"], "T": c["T"],
-                          "pixel_tri_per_s": c["B"] * c["H"] * c["W"] * c["T"] / (m / 1e3)}
-        side["c4_fit_800_iters"] = fit_side(ctx)
         side["c2_torch_fused_mse_fwd_bwd_ms"] = round(torch_op_ms(torch, cfg, p, targets, dev), 4)
         side["c2_torch_rasterize_mse_fwd_bwd_ms"] = round(torch_rasterize_ms(torch, cfg, p, targets, dev), 4)
         side["c2_torch_rasterize_mse_fwd_bwd_rerender_ms"] = round(
             torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=False), 4)
-        side["forward_only"] = forward_side(torch, ctx, dev, cpu=not args.no_cpu_baseline)
+        side["forward_only"] = forward_side(torch, ctx, dev, cpu=cpu)
         out["side"] = side
 
     print(json.dumps(out), flush=True)
