@@ -7,17 +7,21 @@
 //                   integer bounding box exactly as raster.rs:144-168 does,
 //                   the edge vectors and the data for a conservative
 //                   far-outside / deep-inside classification.
-//   raster_kernel : one wave64 per 8x8 pixel tile, four tiles per block.
+//   forward_kernel : one wave64 per 8x8 pixel tile, four tiles per block.
 //                   Each wave compacts the triangles touching its tile into an
 //                   ordered LDS list (ballot + mbcnt), then walks it with the
-//                   triangle record in SGPRs (scalar loads). Sweep 1 composites
-//                   in scene order (raster.rs:46-68). The backward is a second
-//                   sweep in the same order: the gradient reaching layer k,
+//                   triangle record in SGPRs (scalar loads), compositing in
+//                   scene order (raster.rs:46-68); in the gradient modes it
+//                   records the contributing entries with their lane masks
+//                   and each pixel's total transmittance.
+//   backward_kernel : the same tiles, walking the recorded entries again in
+//                   scene order: the gradient reaching layer k,
 //                   d_canvas * prod_{j>k}(1 - w_j) (grad.rs:162-169), is formed
 //                   as a ratio of transmittance products instead of being
-//                   peeled off a tape. Per-triangle gradients are wave-reduced
-//                   with DPP, accumulated per wave in LDS and written as one
-//                   partial row per block.
+//                   peeled off a tape. Per-triangle gradients are summed over
+//                   the wave by a transposition through LDS, accumulated in
+//                   LDS rows and added to the output once per block (or
+//                   written as one partial row per block).
 //   reduce_partials : fixed-order sum of the partial rows, so gradients and
 //                   losses are bit-reproducible run to run.
 //   adam_project  : optim.rs:40-60 followed by fit.rs:399-424, elementwise.
@@ -510,64 +514,13 @@ __device__ inline void exact_cov(const Rec& r, const float* __restrict__ rp, Pix
 
 // ---------------------------------------------------------------- wave reductions
 
-// DPP controls (gfx9 encoding) used below; every source lane is inside the row.
-constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
-constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
-constexpr int DPP_ROW_ROR8 = 0x128;    // row_ror:8, i.e. lane ^ 8 within a row of 16
-constexpr int DPP_HALF_MIRROR = 0x141; // lane -> 7 - lane within each half row of 8
+// DPP controls (gfx9 encoding) used below; every source lane is inside the quad.
+constexpr int DPP_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
 
 template <int ctrl>
 __device__ inline float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
-}
-
-// v_permlane32_swap exchanges the upper half of x with the lower half of y, so
-// the sum gives lanes 0-31 x[l] + x[l+32] and lanes 32-63 y[l-32] + y[l].
-__device__ inline float fold32(float x, float y) {
-    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// v_permlane16_swap exchanges the odd rows of x with the even rows of y: rows
-// 0 and 2 get the row-pair sums of x, rows 1 and 3 those of y.
-__device__ inline float fold16(float x, float y) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Transposed wave64 sum of ten per-lane values. Each folding step halves the
-// lanes a value is spread over while the values share the registers, so the
-// whole reduction is 26 VALU instructions instead of 60 for ten independent
-// trees. The sum of a[p] ends in lane red10_lane(p).
-__device__ inline float wave_reduce10(const float (&a)[NP], int lane) {
-    float b0 = fold32(a[0], a[5]), b1 = fold32(a[1], a[6]), b2 = fold32(a[2], a[7]);
-    float b3 = fold32(a[3], a[8]), b4 = fold32(a[4], a[9]);
-    float c0 = fold16(b0, b1);    // rows hold a0 a1 a5 a6
-    float c1 = fold16(b2, b3);    // rows hold a2 a3 a7 a8
-    float c2 = fold16(b4, 0.0f);  // rows hold a4 -  a9 -
-    const bool h8 = (lane & 8) != 0, h4 = (lane & 4) != 0;
-    float d0 = (h8 ? c1 : c0) + dpp<DPP_ROW_ROR8>(h8 ? c0 : c1);
-    float d1 = c2 + dpp<DPP_ROW_ROR8>(c2);
-    float e = (h4 ? d1 : d0) + dpp<DPP_HALF_MIRROR>(h4 ? d0 : d1);
-    e += dpp<DPP_XOR2>(e);
-    e += dpp<DPP_XOR1>(e);
-    return e;
-}
-// Parameter whose total wave_reduce10 leaves in `lane`, or -1.
-__device__ inline int red10_param(int lane) {
-    const int row = lane >> 4, g = lane & 15;
-    if (g == 0) return row == 0 ? 0 : row == 1 ? 1 : row == 2 ? 5 : 6;
-    if (g == 8) return row == 0 ? 2 : row == 1 ? 3 : row == 2 ? 7 : 8;
-    if (g == 4) return row == 0 ? 4 : row == 2 ? 9 : -1;
-    return -1;
-}
-// Four values (colour and alpha gradients): lane 16 r holds the sum of a_r.
-__device__ inline float wave_reduce4(float a0, float a1, float a2, float a3) {
-    float c = fold16(fold32(a0, a2), fold32(a1, a3));  // rows hold a0 a1 a2 a3
-    c += dpp<DPP_ROW_ROR8>(c);
-    c += dpp<DPP_HALF_MIRROR>(c);
-    c += dpp<DPP_XOR2>(c);
-    c += dpp<DPP_XOR1>(c);
-    return c;
 }
 
 // The wave's lanes for which `c` holds (inactive lanes 0). HIP's __ballot widens
@@ -1075,22 +1028,36 @@ __device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_ban
 }
 
 // Wave sum of the lanes' partial gradients of one triangle, added to its row
-// of the per-wave accumulator. Within a wave the entries are sequential, so
-// each accumulator receives its adds in list order: the sums are reproducible
-// run to run. `any_band` (wave-uniform) says whether any vertex term is set.
-// `slot10` and `slot4` are this lane's accumulator addresses for the 10- and
-// 4-value sums in the row of the first triangle of the chunk; `row_bytes`
-// (uniform) is the triangle's row offset in bytes.
-__device__ inline void reduce_entry(const float (&a)[NP], bool any_band, int row_bytes, lds_float* slot10,
-                                    lds_float* slot4, int lane, int p10) {
-    typedef __attribute__((address_space(3))) char lds_char;
-    if (any_band) {
-        float e = wave_reduce10(a, lane);
-        if (p10 >= 0) lds_add((lds_float*)((lds_char*)slot10 + row_bytes), e);
-    } else {
-        float e = wave_reduce4(a[6], a[7], a[8], a[9]);
-        if ((lane & 15) == 0) lds_add((lds_float*)((lds_char*)slot4 + row_bytes), e);
-    }
+// of an LDS accumulator, by transposition through LDS instead of a shuffle
+// tree: cross-row lane permutes (v_permlane32/16_swap) occupy the SIMD ~8
+// cycles each and DPP ops ~4, plain FP32 adds ~2. Each lane stores its ten
+// values in its column of the wave's area `tw` (ten rows of TP floats); then
+// lane 4p + g (p < 10) sums pixels 16g..16g+15 of parameter p (four 16-byte
+// reads, fifteen adds), a quad DPP sum combines the four partials and lane 4p
+// adds the total into the row. Lanes 40-63 repeat parameter 9's sums (their
+// reads stay in the area) and add nothing. The wave's LDS accesses complete
+// in program order; the fences only keep the compiler from moving them
+// across each other. The sums are in a fixed order, so with a per-wave row
+// (deterministic mode) they are reproducible run to run.
+constexpr int TP = 68;  // row pitch: the reads of the 40 summing lanes fall on all 32 banks
+__device__ inline void reduce_entry(const float (&a)[NP], lds_float* tw, lds_float* row, int lane) {
+    for (int q = 0; q < NP; q++) tw[q * TP + lane] = a[q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int prm = min(lane >> 2, NP - 1), g = lane & 3;
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) f4v lds_f4v;
+    const lds_f4v* src = reinterpret_cast<const lds_f4v*>(tw + prm * TP + 16 * g);
+    const f4v x0 = src[0], x1 = src[1], x2 = src[2], x3 = src[3];
+    float sum = (((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w))) +
+                (((x2.x + x2.y) + (x2.z + x2.w)) + ((x3.x + x3.y) + (x3.z + x3.w)));
+    sum += dpp<DPP_XOR1>(sum);
+    sum += dpp<DPP_XOR2>(sum);
+    if (g == 0 && lane < 4 * NP) lds_add(row + prm, sum);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
@@ -1102,11 +1069,17 @@ __device__ inline void reduce_entry(const float (&a)[NP], bool any_band, int row
 // REBUILD: with the rebuild path for tiles past the recorded entries. Without
 // it (the entries cover T, the usual case) the kernel needs ~55 VGPRs instead
 // of ~95, so it runs uncapped.
-template <int MODE, bool FAST, bool REBUILD>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? 6 : 7))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
+// DET: deterministic mode. Each wave adds into its own accumulator rows and the
+// block sums them in wave order; otherwise the four waves share one set of
+// rows (adds from different waves land in any order, as the float atomics
+// into the output do anyway) and the block needs a quarter of the LDS.
+template <int MODE, bool FAST, bool REBUILD, bool DET>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? (DET ? 4 : 6) : (DET ? 5 : 7)))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
                                                                const TileEnt* __restrict__ ents) {
+    constexpr int ROWS = DET ? WAVES : 1;  // accumulator row sets
     __shared__ uint32_t list[WAVES][CH];
-    __shared__ __attribute__((aligned(16))) float acc[WAVES][CH * NP];
+    __shared__ __attribute__((aligned(16))) float acc[ROWS][CH * NP];
+    __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
     if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
@@ -1137,10 +1110,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     const int cap2 = a.cap2;
     const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
     const size_t blk = tg.tile / WAVES;
-    float* accw = acc[wave];
-    const int p10 = red10_param(lane);
-    lds_float* const slot10 = (lds_float*)accw + (p10 >= 0 ? p10 : 0);
-    lds_float* const slot4 = (lds_float*)accw + 6 + (lane >> 4);
+    float* accw = acc[DET ? wave : 0];
+    lds_float* const tw = (lds_float*)trans[wave];
+    typedef __attribute__((address_space(3))) char lds_char;
     int i2 = 0;
     const bool plain = lane_mask(st.tot.z != 0 || st.tot.e != 0) == 0;
 
@@ -1165,24 +1137,29 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
-            // the recorded byte offset: one add to this lane's address (the product
+            // the recorded byte offset of the triangle's row (the product
             // (k - k0) * NP would become a 64-bit multiply-add on the vector unit)
-            reduce_entry(part, cur.band != 0, (int)cur.row, slot10, slot4, lane, p10);
+            reduce_entry(part, tw, (lds_float*)((lds_char*)accw + cur.row), lane);
         }
     };
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
         int nk = k1 - k0;
-        {
-            // the wave's whole accumulator row (CH * NP floats, 16-byte aligned),
+        if (DET) {
+            // the wave's own accumulator rows (CH * NP floats, 16-byte aligned),
             // four floats per store
             float4* acc4 = reinterpret_cast<float4*>(accw);
             for (int j = lane; j < CH * NP / 4; j += 64) acc4[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        } else {
+            // the block's shared rows, cleared by all its threads
+            float4* acc4 = reinterpret_cast<float4*>(accw);
+            for (int j = threadIdx.x; j < CH * NP / 4; j += WAVES * 64) acc4[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            __syncthreads();
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
         if (c < rec_chunks) {
             if (plain)
@@ -1211,7 +1188,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                 const bool band = __builtin_amdgcn_inverse_ballot_w64(bandm);
                 float part[NP];
                 grad_pixel<false>(r, on, band, any_band, w, cov, g, tg.p, rsig, st, part);
-                reduce_entry(part, any_band, kl * (int)(NP * sizeof(float)), slot10, slot4, lane, p10);
+                reduce_entry(part, tw, (lds_float*)accw + kl * NP, lane);
             }
         }
         __syncthreads();
@@ -1219,18 +1196,17 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
         // Deterministic mode writes them as the block's partial row for
         // reduce_partials; otherwise each nonzero sum is one native float
         // atomic add into the output (one per triangle parameter per block).
-        if (a.deterministic) {
+        if (DET) {
             float* prow = a.partials + (blk * T + k0) * NP;
             for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
                 float v = acc[0][j];
-                for (int q = 1; q < WAVES; q++) v += acc[q][j];
+                for (int q = 1; q < ROWS; q++) v += acc[q][j];
                 prow[j] = v;
             }
         } else {
             float* grow = a.grads + ((size_t)b * T + k0) * NP;
             for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
-                float v = acc[0][j];
-                for (int q = 1; q < WAVES; q++) v += acc[q][j];
+                const float v = acc[0][j];
                 if (v != 0.0f) unsafeAtomicAdd(grow + j, v);
             }
         }
@@ -1238,7 +1214,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     }
     // The per-item loss (canvas.rs:45-58) from the forward kernel's per-block
     // sums, by the scene's first block, in a fixed order.
-    if (MODE == MODE_LOSS && !a.deterministic && tg.bx == 0 && tg.by == 0 && wave == 0) {
+    if (MODE == MODE_LOSS && !DET && tg.bx == 0 && tg.by == 0 && wave == 0) {
         const int nblk = gridDim.x * gridDim.y;
         const double* pl = a.partial_loss + (size_t)b * nblk;
         double l = 0.0;
@@ -1472,13 +1448,6 @@ static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int MODE, bool FAST, bool REBUILD>
-static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s,
-                       a, a.rec, a.tl_ent);
-    return hipGetLastError();
-}
-
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
     if (mode == MODE_RENDER)
         return fast ? launch_forward_t<MODE_RENDER, true>(a, s) : launch_forward_t<MODE_RENDER, false>(a, s);
@@ -1489,15 +1458,30 @@ hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t 
     return fast ? launch_forward_t<MODE_GRAD_IN, true>(a, s) : launch_forward_t<MODE_GRAD_IN, false>(a, s);
 }
 
+template <int MODE, bool FAST, bool REBUILD, bool DET>
+static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD, DET>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0,
+                       s, a, a.rec, a.tl_ent);
+    return hipGetLastError();
+}
+
+template <int MODE, bool FAST, bool REBUILD>
+static hipError_t launch_backward_d(const RasterArgs& a, hipStream_t s) {
+    return a.deterministic ? launch_backward_t<MODE, FAST, REBUILD, true>(a, s)
+                           : launch_backward_t<MODE, FAST, REBUILD, false>(a, s);
+}
+
+template <int MODE, bool FAST>
+static hipError_t launch_backward_r(bool rebuild, const RasterArgs& a, hipStream_t s) {
+    return rebuild ? launch_backward_d<MODE, FAST, true>(a, s) : launch_backward_d<MODE, FAST, false>(a, s);
+}
+
 hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s) {
-    if (rebuild) {
-        if (mode == MODE_LOSS)
-            return fast ? launch_backward_t<MODE_LOSS, true, true>(a, s) : launch_backward_t<MODE_LOSS, false, true>(a, s);
-        return fast ? launch_backward_t<MODE_GRAD_IN, true, true>(a, s) : launch_backward_t<MODE_GRAD_IN, false, true>(a, s);
-    }
     if (mode == MODE_LOSS)
-        return fast ? launch_backward_t<MODE_LOSS, true, false>(a, s) : launch_backward_t<MODE_LOSS, false, false>(a, s);
-    return fast ? launch_backward_t<MODE_GRAD_IN, true, false>(a, s) : launch_backward_t<MODE_GRAD_IN, false, false>(a, s);
+        return fast ? launch_backward_r<MODE_LOSS, true>(rebuild, a, s)
+                    : launch_backward_r<MODE_LOSS, false>(rebuild, a, s);
+    return fast ? launch_backward_r<MODE_GRAD_IN, true>(rebuild, a, s)
+                : launch_backward_r<MODE_GRAD_IN, false>(rebuild, a, s);
 }
 
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
