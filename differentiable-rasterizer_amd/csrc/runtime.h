@@ -163,8 +163,26 @@ struct Out {
 int stage_out(drh_ctx* ctx, Out& o, uint64_t kind, float* dst, size_t n, bool host, hipStream_t s);
 int copy_back(Out& o, hipStream_t s);
 
-// With host pointers or DRH_SYNC: waits for the stream.
+// With host pointers, DRH_SYNC or DRH_PHASES: waits for the stream.
 int finish(uint32_t flags, hipStream_t s);
+
+// Host phases of one call under DRH_PHASES (drh_phases_read). lap() waits for
+// the stream and charges the time since the previous lap to `phase`; publish()
+// makes the laps the calling thread's last phases. Without the flag both do
+// nothing.
+enum Phase : int { PH_PACK = 0, PH_ALLOC, PH_DISPATCH, PH_READBACK, PH_COUNT };
+class PhaseClock {
+  public:
+    PhaseClock(uint32_t flags, hipStream_t s);
+    int lap(int phase);
+    void publish() const;
+
+  private:
+    bool on_;
+    hipStream_t s_;
+    double t_ = 0.0;
+    double ms_[PH_COUNT] = {};
+};
 
 // f32::powi with a runtime exponent (square-and-multiply, as the
 // compiler-builtins __powisf2 that the reference's Adam calls).

@@ -200,8 +200,39 @@ int copy_back(Out& o, hipStream_t s) {
 }
 
 int finish(uint32_t flags, hipStream_t s) {
-    if (flags & (DRH_HOST_PTRS | DRH_SYNC)) return wait_stream(s);
+    if (flags & (DRH_HOST_PTRS | DRH_SYNC | DRH_PHASES)) return wait_stream(s);
     return DRH_OK;
+}
+
+namespace {
+thread_local drh_phase_timings g_phases{};
+
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+}  // namespace
+
+PhaseClock::PhaseClock(uint32_t flags, hipStream_t s) : on_((flags & DRH_PHASES) != 0), s_(s) {
+    if (on_) t_ = now_ms();
+}
+
+int PhaseClock::lap(int phase) {
+    if (!on_) return DRH_OK;
+    int rc = wait_stream(s_);
+    double t = now_ms();
+    ms_[phase] += t - t_;
+    t_ = t;
+    return rc;
+}
+
+void PhaseClock::publish() const {
+    if (!on_) return;
+    g_phases.pack_ms = ms_[PH_PACK];
+    g_phases.alloc_ms = ms_[PH_ALLOC];
+    g_phases.dispatch_ms = ms_[PH_DISPATCH];
+    g_phases.readback_ms = ms_[PH_READBACK];
+    g_phases.loss_ms = 0.0;
+    g_phases.total_ms = ms_[PH_PACK] + ms_[PH_ALLOC] + ms_[PH_DISPATCH] + ms_[PH_READBACK];
 }
 
 float powi_f32(float a, int32_t b) {
@@ -590,6 +621,12 @@ int drh_timing_enable(drh_ctx* ctx, int enable) {
     return DRH_OK;
 }
 
+int drh_phases_read(drh_phase_timings* out) {
+    if (!out) return fail(DRH_ERR_INVALID_ARG, "out is NULL");
+    *out = g_phases;
+    return DRH_OK;
+}
+
 int drh_timing_read(drh_ctx* ctx, drh_timings* out) {
     if (!ctx || !out) return fail(DRH_ERR_INVALID_ARG, "bad arguments");
     std::vector<TimedLaunch> launches;
@@ -634,16 +671,22 @@ int drh_render(drh_ctx* ctx, const float* params, const float* backgrounds, int6
     DeviceGuard dg(ctx->device);
     hipStream_t s = (hipStream_t)stream;
     bool host = flags & DRH_HOST_PTRS;
+    PhaseClock pc(flags, s);
     Staged p, bg;
     Out img;
     if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
     if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = pc.lap(PH_PACK))) return rc;
     if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = pc.lap(PH_ALLOC))) return rc;
     if ((rc = run_raster(ctx, drh::MODE_RENDER, p.dev, bg.dev, nullptr, (int)B, (int)T, (int)H, (int)W, sigma,
                          img.dev, nullptr, nullptr, flags, s)))
         return rc;
+    if ((rc = pc.lap(PH_DISPATCH))) return rc;
     if ((rc = copy_back(img, s))) return rc;
-    return finish(flags, s);
+    if ((rc = finish(flags, s)) || (rc = pc.lap(PH_READBACK))) return rc;
+    pc.publish();
+    return DRH_OK;
 }
 
 int drh_fused_loss_backward(drh_ctx* ctx, const float* params, const float* backgrounds, const float* targets,
@@ -657,19 +700,25 @@ int drh_fused_loss_backward(drh_ctx* ctx, const float* params, const float* back
     DeviceGuard dg(ctx->device);
     hipStream_t s = (hipStream_t)stream;
     bool host = flags & DRH_HOST_PTRS;
+    PhaseClock pc(flags, s);
     Staged p, bg, tg;
     Out losses, grads, img;
     if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
     if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = pc.lap(PH_PACK))) return rc;
     if ((rc = stage_in(ctx, tg, K_IN_IMAGES, targets, (size_t)B * H * W * 3, host, s))) return rc;
     if ((rc = stage_out(ctx, losses, K_OUT_LOSSES, out_losses, (size_t)B, host, s))) return rc;
     if ((rc = stage_out(ctx, grads, K_OUT_GRADS, out_grads, (size_t)B * T * NP, host, s))) return rc;
     if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
+    if ((rc = pc.lap(PH_ALLOC))) return rc;
     if ((rc = run_raster(ctx, drh::MODE_LOSS, p.dev, bg.dev, tg.dev, (int)B, (int)T, (int)H, (int)W, sigma, img.dev,
                          grads.dev, losses.dev, flags, s)))
         return rc;
+    if ((rc = pc.lap(PH_DISPATCH))) return rc;
     if ((rc = copy_back(losses, s)) || (rc = copy_back(grads, s)) || (rc = copy_back(img, s))) return rc;
-    return finish(flags, s);
+    if ((rc = finish(flags, s)) || (rc = pc.lap(PH_READBACK))) return rc;
+    pc.publish();
+    return DRH_OK;
 }
 
 int drh_backward_from_grad(drh_ctx* ctx, const float* params, const float* backgrounds, const float* grad_images,
@@ -682,17 +731,23 @@ int drh_backward_from_grad(drh_ctx* ctx, const float* params, const float* backg
     DeviceGuard dg(ctx->device);
     hipStream_t s = (hipStream_t)stream;
     bool host = flags & DRH_HOST_PTRS;
+    PhaseClock pc(flags, s);
     Staged p, bg, gi;
     Out grads;
     if ((rc = stage_in(ctx, p, K_IN_PARAMS, params, (size_t)B * T * NP, host, s))) return rc;
     if ((rc = stage_in(ctx, bg, K_IN_BG, backgrounds, (size_t)B * 3, host, s))) return rc;
+    if ((rc = pc.lap(PH_PACK))) return rc;
     if ((rc = stage_in(ctx, gi, K_IN_IMAGES, grad_images, (size_t)B * H * W * 3, host, s))) return rc;
     if ((rc = stage_out(ctx, grads, K_OUT_GRADS, out_grads, (size_t)B * T * NP, host, s))) return rc;
+    if ((rc = pc.lap(PH_ALLOC))) return rc;
     if ((rc = run_raster(ctx, drh::MODE_GRAD_IN, p.dev, bg.dev, gi.dev, (int)B, (int)T, (int)H, (int)W, sigma,
                          nullptr, grads.dev, nullptr, flags, s)))
         return rc;
+    if ((rc = pc.lap(PH_DISPATCH))) return rc;
     if ((rc = copy_back(grads, s))) return rc;
-    return finish(flags, s);
+    if ((rc = finish(flags, s)) || (rc = pc.lap(PH_READBACK))) return rc;
+    pc.publish();
+    return DRH_OK;
 }
 
 int drh_record_bytes(int64_t B, int64_t T, int64_t H, int64_t W, uint64_t* out_bytes) {

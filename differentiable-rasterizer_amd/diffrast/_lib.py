@@ -30,6 +30,7 @@ SYNC = 0x2
 EXACT_MATH = 0x4
 DETERMINISTIC = 0x8
 CHANNELS_FIRST = 0x10
+PHASES = 0x20
 
 STOP_REASONS = {0: "Completed", 1: "Converged", 2: "Diverged"}
 CONFIG_ERRORS = {1: "NoTriangles", 2: "NonPositiveSigma", 3: "SigmaNotDecreasing",
@@ -86,6 +87,11 @@ class Timings(ctypes.Structure):
     ]
 
 
+class PhaseTimings(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_double) for name in
+                ("pack_ms", "alloc_ms", "dispatch_ms", "readback_ms", "loss_ms", "total_ms")]
+
+
 class StepInfo(ctypes.Structure):
     _fields_ = [("iter", ctypes.c_int64), ("loss", ctypes.c_float), ("sigma", ctypes.c_float)]
 
@@ -105,6 +111,7 @@ class FitStatus(ctypes.Structure):
 SIGNATURES = {
     "drh_timing_enable": ([_P, ctypes.c_int], ctypes.c_int),
     "drh_timing_read": ([_P, ctypes.POINTER(Timings)], ctypes.c_int),
+    "drh_phases_read": ([ctypes.POINTER(PhaseTimings)], ctypes.c_int),
     "drh_create": ([ctypes.POINTER(_P)], ctypes.c_int),
     "drh_destroy": ([_P], ctypes.c_int),
     "drh_last_error": ([], ctypes.c_char_p),
@@ -253,6 +260,13 @@ class Context:
         check(lib().drh_timing_read(self.handle, ctypes.byref(t)))
         return {name: getattr(t, name) for name, _ in Timings._fields_}
 
+    @staticmethod
+    def read_phases() -> dict:
+        """Host phases of this thread's last call made with the PHASES flag."""
+        t = PhaseTimings()
+        check(lib().drh_phases_read(ctypes.byref(t)))
+        return {name: getattr(t, name) for name, _ in PhaseTimings._fields_}
+
     # -- device-pointer forms (asynchronous on `stream`) ---------------------
     def render_ptr(self, params, bgs, B, T, H, W, sigma, out, stream=None, flags=0):
         check(lib().drh_render(self.handle, params, bgs, B, T, H, W, sigma, out, stream, flags))
@@ -328,6 +342,20 @@ class Context:
                        _ptr(imgs), flags=HOST_PTRS | (EXACT_MATH if exact else 0) |
                        (DETERMINISTIC if deterministic else 0))
         return (losses, grads, imgs) if want_images else (losses, grads)
+
+    def backward_many_timed(self, params, targets, sigma: float, background=(0, 0, 0)):
+        """fused_loss_backward with its host phases (GpuRasterizer::backward_many_timed,
+        crates/diffrast-gpu/src/lib.rs:649-664): (losses, grads, phases). The stream is
+        drained between phases, so the total bounds the untimed call from above."""
+        p, t = _f32(params), _f32(targets)
+        B, T = p.shape[0], p.shape[1]
+        H, W = t.shape[1], t.shape[2]
+        bgs = _bgs(background, B)
+        losses = np.empty(B, np.float32)
+        grads = np.empty((B, T, 10), np.float32)
+        self.fused_ptr(_ptr(p), _ptr(bgs), _ptr(t), B, T, H, W, sigma, _ptr(losses), _ptr(grads),
+                       None, flags=HOST_PTRS | PHASES)
+        return losses, grads, self.read_phases()
 
     def backward_from_grad(self, params, grad_images, sigma: float, background=(0, 0, 0),
                            exact: bool = False, deterministic: bool = False) -> np.ndarray:

@@ -52,6 +52,8 @@ enum {
                                   (default: one float atomic per triangle parameter per block) */
 #define DRH_CHANNELS_FIRST 0x10u /* images, targets and grad_images are B x 3 x H x W (the
                                     layout torch_layer.rasterize returns) instead of B x H x W x 3 */
+#define DRH_PHASES 0x20u  /* drh_render, drh_fused_loss_backward, drh_backward_from_grad: wait for
+                             the stream between phases and keep their host times (drh_phases_read) */
 
 /* Bounded host wait, as GpuRasterizer::POLL_TIMEOUT (crates/diffrast-gpu/src/lib.rs:229). */
 #define DRH_WAIT_TIMEOUT_S 60
@@ -97,6 +99,27 @@ typedef struct {
 
 int drh_timing_enable(drh_ctx *ctx, int enable);
 int drh_timing_read(drh_ctx *ctx, drh_timings *out);
+
+/* Host wall-clock phases of one call made with DRH_PHASES: BackwardTimings
+ * (crates/diffrast-gpu/src/lib.rs:96-114) as backward_many_timed
+ * (lib.rs:649-664) measures it, by waiting for the stream between phases, so
+ * the total is an upper bound on the call without the flag.
+ *   pack_ms      pooled device buffers for params and backgrounds taken and
+ *                filled (0 with device pointers)
+ *   alloc_ms     pooled buffers for targets / upstream gradients (filled),
+ *                images, gradients and losses taken
+ *   dispatch_ms  every kernel enqueued and finished (all device execution)
+ *   readback_ms  results copied back to the host
+ *   loss_ms      per-item loss on the host: always 0, the loss is reduced on
+ *                the device inside dispatch
+ *   total_ms     the sum of the five, BackwardTimings::total_ms */
+typedef struct {
+    double pack_ms, alloc_ms, dispatch_ms, readback_ms, loss_ms, total_ms;
+} drh_phase_timings;
+
+/* The phases of the calling thread's last DRH_PHASES call (zeros before the
+ * first). */
+int drh_phases_read(drh_phase_timings *out);
 
 /* Batched forward render: render_many (crates/diffrast-gpu/src/lib.rs:615-633)
  * and render_batch (crates/diffrast-py/src/lib.rs:174-231), per-pixel

@@ -227,6 +227,25 @@ def test_pool_reuses_buffers_across_identical_calls(ctx):  # crates/diffrast-gpu
     assert ctx.pool_stats()["bytes"] == 0
 
 
+def test_backward_many_timed_reports_host_phases(ctx):  # crates/diffrast-gpu/src/lib.rs:96-114, 649-664
+    from diffrast import _lib
+
+    params = synth.batch("uniform", 4, 64, 17)
+    targets = np.stack([synth.blob_target(70 + b, 96, 96) for b in range(4)])
+    plain = ctx.fused_loss_backward(params, targets, 0.004, deterministic=True)
+    losses, grads, ph = ctx.backward_many_timed(params, targets, 0.004)
+    print("phases (ms):", {k: round(v, 3) for k, v in ph.items()}, flush=True)
+    assert np.array_equal(losses, plain[0])
+    assert grad_err(grads, plain[1]) <= 1e-6
+    parts = ("pack_ms", "alloc_ms", "dispatch_ms", "readback_ms", "loss_ms")
+    assert all(ph[k] >= 0.0 for k in parts) and ph["loss_ms"] == 0.0
+    assert ph["dispatch_ms"] > 0.0 and ph["readback_ms"] > 0.0
+    assert ph["total_ms"] == pytest.approx(sum(ph[k] for k in parts), rel=1e-12)
+    # the phases stay those of the last timed call: an untimed call leaves them
+    ctx.fused_loss_backward(params, targets, 0.004)
+    assert _lib.Context.read_phases() == ph
+
+
 def test_pool_buffers_move_between_streams(ctx):
     # Pooled buffers used on one stream, then on others (device pointers,
     # asynchronous calls): results identical to a single-stream run.
