@@ -307,4 +307,17 @@ extern "C" {
         stream: *mut c_void,
         flags: u32,
     ) -> c_int;
+
+    pub fn drh_resize_lanczos3(
+        ctx: *mut drh_ctx,
+        src: *const u8,
+        h: i64,
+        w: i64,
+        c: i64,
+        dst: *mut u8,
+        new_h: i64,
+        new_w: i64,
+        stream: *mut c_void,
+        flags: u32,
+    ) -> c_int;
 }

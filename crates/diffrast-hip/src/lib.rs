@@ -581,6 +581,45 @@ impl GpuRasterizer {
         Ok(out)
     }
 
+    /// The resample of `Canvas::load_image` (canvas.rs:71-79): image 0.25's
+    /// `resize_exact(new_width, new_height, FilterType::Lanczos3)` of a
+    /// `height x width x channels` byte image (channels 1-4), bit for bit.
+    /// Feed the result to [`Self::decode_srgb`] for the linear canvas.
+    pub fn resize_lanczos3(
+        &self,
+        image: &[u8],
+        width: usize,
+        height: usize,
+        channels: usize,
+        new_width: usize,
+        new_height: usize,
+    ) -> Result<Vec<u8>, GpuError> {
+        if image.len() != width * height * channels {
+            return Err(GpuError::TooLarge(format!(
+                "expected {} bytes for {width}x{height}x{channels}, got {}",
+                width * height * channels,
+                image.len()
+            )));
+        }
+        let mut out = vec![0u8; new_width * new_height * channels];
+        // SAFETY: host arrays of the sizes the call reads and writes.
+        check(unsafe {
+            ffi::drh_resize_lanczos3(
+                self.raw(),
+                image.as_ptr(),
+                height as i64,
+                width as i64,
+                channels as i64,
+                out.as_mut_ptr(),
+                new_height as i64,
+                new_width as i64,
+                ptr::null_mut(),
+                ffi::DRH_HOST_PTRS,
+            )
+        })?;
+        Ok(out)
+    }
+
     /// A step-wise fit on this device (`diffrast::Fitter::new`, fit.rs:214-237).
     pub fn fitter(&self, target: Canvas, cfg: FitConfig) -> Result<Fitter<'_>, FitError> {
         Fitter::on(self, target, cfg)

@@ -18,7 +18,7 @@ CSRC = HERE / "csrc"
 LIB = HERE / "libdiffrast_hip.so"
 ARCH = os.environ.get("DIFFRAST_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = [CSRC / "kernels.hip", CSRC / "runtime.hip", CSRC / "fit.hip", CSRC / "scratch.hip"]
+SOURCES = [CSRC / "kernels.hip", CSRC / "runtime.hip", CSRC / "fit.hip", CSRC / "scratch.hip", CSRC / "resize.hip"]
 HEADERS = [CSRC / "kernels.h", CSRC / "runtime.h", ROOT / "include" / "diffrast_hip.h"]
 
 # -ffp-contract=off: the kernels state every FMA explicitly; plain a*b+c must

@@ -1,6 +1,7 @@
 // Internal declarations shared by the host sources behind the C ABI
 // (runtime.hip: context, pool, raster entry points; fit.hip: the fit loop and
-// the step-wise fitter; scratch.hip: the entry point that allocates nothing).
+// the step-wise fitter; scratch.hip: the entry point that allocates nothing;
+// resize.hip: the Lanczos3 image resize).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -49,6 +50,9 @@ enum Kind : uint64_t {
     K_SRGB_U8,
     K_ORDER,
     K_FIT_TARGET,
+    K_RESIZE_U8,
+    K_RESIZE_TAB,
+    K_RESIZE_TMP,
 };
 
 // Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers

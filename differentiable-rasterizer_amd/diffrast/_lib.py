@@ -149,6 +149,7 @@ SIGNATURES = {
                               ctypes.c_int),
     "drh_encode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
     "drh_decode_srgb": ([_P, _P, _I64, _P, _P, _U32], ctypes.c_int),
+    "drh_resize_lanczos3": ([_P, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _U32], ctypes.c_int),
 }
 
 _lib = None
@@ -304,7 +305,22 @@ class Context:
     def decode_srgb_ptr(self, data, n, out, stream=None, flags=0):
         check(lib().drh_decode_srgb(self.handle, data, n, out, stream, flags))
 
+    def resize_lanczos3_ptr(self, src, H, W, C, dst, new_H, new_W, stream=None, flags=0):
+        check(lib().drh_resize_lanczos3(self.handle, src, H, W, C, dst, new_H, new_W, stream, flags))
+
     # -- host (numpy) forms, synchronous --------------------------------------
+    def resize_lanczos3(self, image, width: int, height: int) -> np.ndarray:
+        """Canvas::load_image's resize_exact(width, height, Lanczos3) (canvas.rs:71-79) of an
+        (H, W, C) uint8 image."""
+        a = np.ascontiguousarray(image, dtype=np.uint8)
+        if a.ndim != 3:
+            raise ValueError(f"expected an (H, W, C) image, got shape {a.shape}")
+        H, W, C = a.shape
+        out = np.empty((height, width, C), np.uint8)
+        self.resize_lanczos3_ptr(a.ctypes.data_as(ctypes.c_void_p), H, W, C, out.ctypes.data_as(ctypes.c_void_p),
+                                 height, width, flags=HOST_PTRS)
+        return out
+
     def encode_srgb(self, values) -> np.ndarray:
         """canvas.rs:100-105 per value: linear float32 to sRGB bytes, same shape."""
         v = _f32(values)

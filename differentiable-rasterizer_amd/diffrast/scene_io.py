@@ -9,8 +9,9 @@
   `drh_encode_srgb` / `drh_decode_srgb`, bit-identical to the reference; the PNG
   container is written and read here over zlib (8-bit RGB out; 8-bit gray, RGB,
   palette, gray+alpha and RGBA in, alpha dropped as `to_rgb8` drops it).
-  `load_image`'s Lanczos3 resize to another size is not provided: `load_png` reads
-  an image at its own size.
+  `load_png(path, width, height)` resamples to another size first, as `load_image`
+  does, with image 0.25's Lanczos3 `resize_exact` on the GPU (`drh_resize_lanczos3`);
+  `load_target` is the fit binary's target loading (aspect kept by `fit_within`).
 """
 
 from __future__ import annotations
@@ -318,15 +319,35 @@ def save_png(path, image) -> None:
     write_png(path, b)
 
 
-def load_png(path, width: int | None = None, height: int | None = None) -> np.ndarray:
-    """Canvas::load_image (canvas.rs:70-86) at the file's own size: (H, W, 3) linear
-    float32. A requested size other than the file's is refused (the reference
-    resamples with Lanczos3, which this build does not provide)."""
+def _read(path) -> np.ndarray:
     try:
-        rgb = read_png(path)
+        return read_png(path)
     except OSError as exc:
         raise FitError(f"cannot read {path}: {exc}") from exc
-    h, w = rgb.shape[0], rgb.shape[1]
-    if (width is not None and width != w) or (height is not None and height != h):
-        raise FitError(f"{path} is {w}x{h}; resampling to {width}x{height} is not provided")
+
+
+def _linear(rgb: np.ndarray, width: int, height: int):
+    """Bytes resampled to width x height (image 0.25's Lanczos3 resize_exact, on the
+    GPU via drh_resize_lanczos3; the same size is left as is), then decoded."""
+    if width <= 0 or height <= 0:
+        raise FitError(f"cannot resize to {width}x{height}")
+    if (width, height) != (rgb.shape[1], rgb.shape[0]):
+        rgb = _context().resize_lanczos3(rgb, width, height)
     return decode_srgb(rgb)
+
+
+def load_png(path, width: int | None = None, height: int | None = None) -> np.ndarray:
+    """Canvas::load_image (canvas.rs:70-86): an (H, W, 3) linear float32 image at
+    width x height (default: the file's size)."""
+    rgb = _read(path)
+    h, w = rgb.shape[0], rgb.shape[1]
+    return _linear(rgb, w if width is None else int(width), h if height is None else int(height))
+
+
+def load_target(path, size: int) -> np.ndarray:
+    """The fit binary's target loading (crates/diffrast/src/bin/fit.rs:186-196): the file
+    scaled so neither side exceeds `size`, keeping its aspect ratio (fit_within)."""
+    if not Path(path).exists():
+        raise FitError(f"no such file: {path}")
+    rgb = _read(path)
+    return _linear(rgb, *fit_within(rgb.shape[1], rgb.shape[0], size))

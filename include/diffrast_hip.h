@@ -317,6 +317,15 @@ int drh_encode_srgb(drh_ctx *ctx, const float *values, int64_t n, uint8_t *out, 
 int drh_decode_srgb(drh_ctx *ctx, const uint8_t *bytes, int64_t n, float *out, void *stream,
                     uint32_t flags);
 
+/* The resize of Canvas::load_image (canvas.rs:71-79): `resize_exact(new_W,
+ * new_H, FilterType::Lanczos3)` of image 0.25.10 (Cargo.lock:410-411) on an
+ * H x W x C byte image (C in 1..4, channels resampled independently) into
+ * new_H x new_W x C bytes; the same size is a copy. The weights are built on
+ * the host, so the call waits for the stream before returning whenever it
+ * resamples. */
+int drh_resize_lanczos3(drh_ctx *ctx, const uint8_t *src, int64_t H, int64_t W, int64_t C, uint8_t *dst,
+                        int64_t new_H, int64_t new_W, void *stream, uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -742,3 +742,89 @@ uint64_t orc_srgb_encode_scan(float thresholds[256]) {
     }
     return drops;
 }
+
+/* ------------------------------------------------------------------------
+ * Lanczos3 resize: image 0.25.10 imageops::resize (sample.rs: resize,
+ * vertical_sample, horizontal_sample, lanczos3_kernel), the resample of
+ * Canvas::load_image (canvas.rs:71-79). The crate is not in the reference
+ * tree; this follows its published source. f32 throughout, glibc sinf (the
+ * libm behind Rust's f32::sin on Linux), products and sums unfused.
+ * ------------------------------------------------------------------------ */
+
+/* sinc with f32::consts::PI; 1 at 0. */
+static float sinc_f32(float t) {
+    const float a = t * 3.14159265358979323846f;
+    return t == 0.0f ? 1.0f : sinf(a) / a;
+}
+
+float orc_lanczos3(float x) {
+    return fabsf(x) < 3.0f ? sinc_f32(x) * sinc_f32(x / 3.0f) : 0.0f;
+}
+
+size_t orc_lanczos3_taps(size_t n_src, size_t n_dst, size_t o, size_t *left, float *w, size_t cap) {
+    const float ratio = (float)n_src / (float)n_dst;
+    const float scale = ratio < 1.0f ? 1.0f : ratio;
+    const float support = 3.0f * scale;
+    const float centre = ((float)o + 0.5f) * ratio;
+    int64_t lo = (int64_t)floorf(centre - support);
+    if (lo < 0) lo = 0;
+    if (lo > (int64_t)n_src - 1) lo = (int64_t)n_src - 1;
+    int64_t hi = (int64_t)ceilf(centre + support);
+    if (hi < lo + 1) hi = lo + 1;
+    if (hi > (int64_t)n_src) hi = (int64_t)n_src;
+    const size_t count = (size_t)(hi - lo);
+    if (count > cap) return 0;
+    const float c = centre - 0.5f;
+    float sum = 0.0f;
+    for (size_t k = 0; k < count; k++) {
+        w[k] = orc_lanczos3(((float)(lo + (int64_t)k) - c) / scale);
+        sum += w[k];
+    }
+    for (size_t k = 0; k < count; k++) w[k] /= sum;
+    *left = (size_t)lo;
+    return count;
+}
+
+void orc_resize_lanczos3(const uint8_t *src, size_t W, size_t H, size_t C, uint8_t *dst, size_t new_W,
+                         size_t new_H) {
+    if (W == 0 || H == 0 || new_W == 0 || new_H == 0) return;
+    if (W == new_W && H == new_H) {
+        memcpy(dst, src, W * H * C);
+        return;
+    }
+    const size_t vcap = (size_t)(6.0f * ((float)H / (float)new_H < 1.0f ? 1.0f : (float)H / (float)new_H)) + 3;
+    const size_t hcap = (size_t)(6.0f * ((float)W / (float)new_W < 1.0f ? 1.0f : (float)W / (float)new_W)) + 3;
+    float *tmp = malloc(sizeof(float) * new_H * W * C);
+    float *w = malloc(sizeof(float) * (vcap > hcap ? vcap : hcap));
+    if (!tmp || !w) {
+        free(tmp);
+        free(w);
+        return;
+    }
+    /* vertical: bytes -> f32 rows, new_H x W x C */
+    for (size_t oy = 0; oy < new_H; oy++) {
+        size_t lo = 0;
+        const size_t n = orc_lanczos3_taps(H, new_H, oy, &lo, w, vcap);
+        for (size_t e = 0; e < W * C; e++) {
+            float t = 0.0f;
+            for (size_t k = 0; k < n; k++) t += (float)src[(lo + k) * W * C + e] * w[k];
+            tmp[oy * W * C + e] = t;
+        }
+    }
+    /* horizontal: f32 rows -> bytes, clamped to [0, 255], rounded half away from zero */
+    for (size_t ox = 0; ox < new_W; ox++) {
+        size_t lo = 0;
+        const size_t n = orc_lanczos3_taps(W, new_W, ox, &lo, w, hcap);
+        for (size_t y = 0; y < new_H; y++) {
+            for (size_t c = 0; c < C; c++) {
+                float t = 0.0f;
+                for (size_t k = 0; k < n; k++) t += tmp[(y * W + lo + k) * C + c] * w[k];
+                if (t < 0.0f) t = 0.0f;
+                if (t > 255.0f) t = 255.0f;
+                dst[(y * new_W + ox) * C + c] = (uint8_t)roundf(t);
+            }
+        }
+    }
+    free(tmp);
+    free(w);
+}

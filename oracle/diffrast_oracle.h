@@ -140,6 +140,25 @@ void orc_decode_srgb(const uint8_t *v, size_t n, float *out);
  * (thresholds[0] = 0). */
 uint64_t orc_srgb_encode_scan(float thresholds[256]);
 
+/* The resize of Canvas::load_image (canvas.rs:71-79): image 0.25.10's
+ * imageops::resize with FilterType::Lanczos3 (Cargo.lock:410-411; the crate is
+ * not in the reference tree, so this restates its published algorithm).
+ * Separable: a vertical pass from bytes to f32 rows, then a horizontal pass
+ * that clamps to [0, 255] and rounds half away from zero; the same size is a
+ * plain copy. Each output index o of a pass over n_src -> n_dst samples
+ * reads the source indices [left, left + count) with weights that sum to 1:
+ *   ratio = n_src / n_dst, scale = max(ratio, 1), support = 3 * scale,
+ *   centre = (o + 0.5) * ratio,
+ *   left = clamp(floor(centre - support), 0, n_src - 1),
+ *   right = clamp(ceil(centre + support), left + 1, n_src),
+ *   w_i = lanczos3((i - (centre - 0.5)) / scale) / sum, all in f32.
+ * orc_lanczos3_taps writes left and at most `cap` weights and returns count
+ * (0 if cap is too small). Images are H x W x C bytes, C in 1..4. */
+float orc_lanczos3(float x);
+size_t orc_lanczos3_taps(size_t n_src, size_t n_dst, size_t o, size_t *left, float *w, size_t cap);
+void orc_resize_lanczos3(const uint8_t *src, size_t W, size_t H, size_t C, uint8_t *dst, size_t new_W,
+                         size_t new_H);
+
 #ifdef __cplusplus
 }
 #endif

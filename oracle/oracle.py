@@ -102,6 +102,11 @@ def lib() -> ctypes.CDLL:
         L.orc_decode_srgb.argtypes = [_U8, _SZ, _F]
         L.orc_srgb_encode_scan.argtypes = [_F]
         L.orc_srgb_encode_scan.restype = ctypes.c_uint64
+        L.orc_lanczos3.argtypes = [ctypes.c_float]
+        L.orc_lanczos3.restype = ctypes.c_float
+        L.orc_lanczos3_taps.argtypes = [_SZ, _SZ, _SZ, ctypes.POINTER(ctypes.c_size_t), _F, _SZ]
+        L.orc_lanczos3_taps.restype = _SZ
+        L.orc_resize_lanczos3.argtypes = [_U8, _SZ, _SZ, _SZ, _U8, _SZ, _SZ]
         _lib = L
     return _lib
 
@@ -345,3 +350,28 @@ def srgb_encode_scan():
     thr = np.zeros(256, np.float32)
     drops = lib().orc_srgb_encode_scan(_p(thr))
     return int(drops), thr
+
+
+def lanczos3(x: float) -> float:
+    """image 0.25.10 lanczos3_kernel in f32."""
+    return float(lib().orc_lanczos3(x))
+
+
+def lanczos3_taps(n_src: int, n_dst: int, o: int):
+    """(left, weights) of output index o of one resize pass."""
+    cap = 64 + int(6 * max(n_src / n_dst, 1.0))
+    w = np.zeros(cap, np.float32)
+    left = ctypes.c_size_t(0)
+    n = lib().orc_lanczos3_taps(n_src, n_dst, o, ctypes.byref(left), _p(w), cap)
+    assert n > 0
+    return int(left.value), w[:n].copy()
+
+
+def resize_lanczos3(img, width: int, height: int) -> np.ndarray:
+    """Canvas::load_image's resize_exact(width, height, Lanczos3) of an (H, W, C) uint8 image."""
+    a = np.ascontiguousarray(img, dtype=np.uint8)
+    H, W, C = a.shape
+    out = np.zeros((height, width, C), np.uint8)
+    u8 = ctypes.POINTER(ctypes.c_uint8)
+    lib().orc_resize_lanczos3(a.ctypes.data_as(u8), W, H, C, out.ctypes.data_as(u8), width, height)
+    return out

@@ -159,6 +159,23 @@ int main(void) {
         orc_decode_srgb(bytes, 256, vals);
         (void)orc_srgb_encode_scan(thr);
     }
+    /* Lanczos3 resize: shrink, grow, one axis, 1x1, same size, every channel count */
+    {
+        const size_t cases[][4] = {{40, 30, 15, 20}, {7, 9, 64, 5}, {1, 1, 3, 4}, {33, 47, 33, 47}, {300, 2, 1, 3}};
+        for (size_t k = 0; k < sizeof cases / sizeof cases[0]; k++) {
+            for (size_t C = 1; C <= 4; C++) {
+                const size_t W = cases[k][0], H = cases[k][1], nW = cases[k][2], nH = cases[k][3];
+                uint8_t *src = xmalloc(W * H * C), *dst = xmalloc(nW * nH * C);
+                for (size_t i = 0; i < W * H * C; i++) src[i] = (uint8_t)(urand() * 255.0f);
+                orc_resize_lanczos3(src, W, H, C, dst, nW, nH);
+                free(src);
+                free(dst);
+            }
+        }
+        size_t left = 0;
+        float w[64];
+        if (orc_lanczos3_taps(100, 3, 1, &left, w, 4) != 0) return 1; /* too small a buffer is refused */
+    }
     printf("ok\n");
     return 0;
 }

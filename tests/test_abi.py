@@ -22,7 +22,7 @@ def L():
 def declared_symbols():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(drh_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(drh_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_boundary():

@@ -81,8 +81,53 @@ def test_png_files_round_trip_the_reference_fit_target(tmp_path, orc):
     out = tmp_path / "again.png"
     scene_io.save_png(out, lin)
     assert np.array_equal(scene_io.read_png(out), raw)  # decode then encode is the identity
+
+
+@pytest.mark.parametrize("size", [(64, 64), (100, 37), (176, 90), (301, 512), (176, 176)])
+def test_load_png_resamples_like_the_oracle(orc, size):  # canvas.rs:71-87
+    from diffrast import scene_io
+
+    src = GOLDEN / "fit_target_176.png"
+    raw = scene_io.read_png(src)
+    lin = scene_io.load_png(src, *size)
+    assert lin.shape == (size[1], size[0], 3)
+    assert np.array_equal(lin, orc.decode_srgb(orc.resize_lanczos3(raw, *size)))
+
+
+def test_load_target_keeps_the_aspect_ratio(orc, tmp_path):  # crates/diffrast/src/bin/fit.rs:186-196
+    from diffrast import scene_io
+
+    rng = np.random.default_rng(3)
+    wide = rng.integers(0, 256, (120, 300, 3), dtype=np.uint8)
+    scene_io.write_png(tmp_path / "wide.png", wide)
+    t = scene_io.load_target(tmp_path / "wide.png", 176)
+    assert t.shape == (70, 176, 3)  # fit_within(300, 120, 176)
+    assert np.array_equal(t, orc.decode_srgb(orc.resize_lanczos3(wide, 176, 70)))
+    small = scene_io.load_target(tmp_path / "wide.png", 1000)  # never scaled up
+    assert np.array_equal(small, orc.decode_srgb(wide))
     with pytest.raises(scene_io.FitError):
-        scene_io.load_png(src, 64, 64)
+        scene_io.load_target(tmp_path / "missing.png", 176)
+
+
+@pytest.mark.parametrize("shape,size", [((480, 640, 3), (176, 132)), ((33, 47, 4), (141, 99)), ((64, 64, 1), (17, 5)),
+                                        ((2000, 3, 3), (1, 700)), ((1, 1, 3), (9, 4)), ((70000, 2, 1), (3, 70001))])
+def test_resize_matches_the_oracle(ctx, orc, shape, size):
+    rng = np.random.default_rng(shape[0] + size[0])
+    img = rng.integers(0, 256, shape, dtype=np.uint8)
+    print(f"resize {shape} -> {size}", flush=True)
+    assert np.array_equal(ctx.resize_lanczos3(img, *size), orc.resize_lanczos3(img, *size))
+
+
+def test_resize_rejects_bad_arguments(ctx):
+    from diffrast import _lib
+
+    img = np.zeros((8, 8, 5), np.uint8)
+    with pytest.raises(_lib.DiffrastError) as e:
+        ctx.resize_lanczos3(img, 4, 4)
+    assert e.value.code == 6
+    with pytest.raises(_lib.DiffrastError) as e:
+        ctx.resize_lanczos3(np.zeros((8, 8, 3), np.uint8), 0, 4)
+    assert e.value.code == 6
 
 
 def test_saved_render_matches_the_oracle_bytes(ctx, orc, tmp_path):
