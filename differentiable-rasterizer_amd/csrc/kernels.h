@@ -104,7 +104,21 @@ struct RasterArgs {
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
     const int* perm_bwd;   // block order of the backward kernel or null
     const int* halt;       // null, or a flag: every block returns at entry once it is >= 0
+    // Split backward (nseg > 1, with a block order): in the nsplit heaviest
+    // blocks of each scene, segment s of a tile's recorded entries,
+    // [s seg_m, (s + 1) seg_m) (the last one to the end), is swept by its own
+    // wave, starting from the pixel state the forward kernel checkpointed
+    // before entry s seg_m: ckpt holds CKPT_WORDS x 64 words per (tile, s >= 1).
+    int nseg;              // segments per split tile, 0 or 1: no split
+    int seg_m;             // entries per segment
+    int nsplit;            // split blocks per scene
+    int gx, gy;            // blocks per scene row and column
+    float* ckpt;           // ntiles * (nseg - 1) * CKPT_WORDS * 64
 };
+
+// A checkpoint word per lane: colour (3), transmittance q, zero count z and
+// rescaling count e (as int bits).
+constexpr int CKPT_WORDS = 6;
 
 // Head of a forward record (drh_render_record), written by setup_records:
 // what a later backward of the record must agree with.

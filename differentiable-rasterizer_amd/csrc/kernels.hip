@@ -32,6 +32,7 @@
 // the stated tolerance (gradient assembly, conservative classification).
 
 #include <hip/hip_runtime.h>
+#include <climits>
 #include <stdint.h>
 #include <type_traits>
 
@@ -775,32 +776,28 @@ __device__ inline size_t img_index(const RasterArgs& a, size_t pix, int b, int c
 }
 
 // Tile geometry shared by both kernels: one wave per 8x8 tile, four tiles
-// (2x2) per block, one pixel per lane.
+// (2x2) per block, one pixel per lane. `rank`: the block's place in the block
+// order (-1 without one); `seg` of `nseg`: the backward segment.
 struct TileGeo {
-    int lane, wave, b, bx, by, x, y, tx0, ty0, tx1, ty1;
+    int lane, wave, b, rank, seg, nseg, bx, by, x, y, tx0, ty0, tx1, ty1;
     bool valid, live;
     Pix p;
     float cx0, cy0, cx1, cy1;
     size_t pix, tile;
 };
 
-// With `perm` (setup_records' block order of B scenes) launch slot i (scene-major
-// linear index) works on block perm[s * nb + i / B] of scene s = i % B.
-__device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int B = 1) {
+// The tile of this wave in block (bx, by) of scene b, gx x gy blocks per scene.
+__device__ inline TileGeo tile_at(int W, int H, int gx, int gy, int b, int bx, int by, int rank, int seg,
+                                  int nseg) {
     TileGeo t;
     t.lane = threadIdx.x & 63;
     t.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile indices
-    t.bx = blockIdx.x;
-    t.by = blockIdx.y;
-    t.b = blockIdx.z;
-    if (perm) {
-        const int nb = (int)(gridDim.x * gridDim.y);
-        const int i = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-        t.b = i % B;
-        const int local = min(max(perm[(size_t)t.b * nb + i / B], 0), nb - 1);
-        t.bx = local % (int)gridDim.x;
-        t.by = local / (int)gridDim.x;
-    }
+    t.b = b;
+    t.rank = rank;
+    t.seg = seg;
+    t.nseg = nseg;
+    t.bx = bx;
+    t.by = by;
     t.tx0 = (t.bx * 2 + (t.wave & 1)) * TILE;
     t.ty0 = (t.by * 2 + (t.wave >> 1)) * TILE;
     t.x = t.tx0 + (t.lane & 7);
@@ -818,8 +815,44 @@ __device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int 
     t.cx1 = ((float)(t.tx1 - 1) + 0.5f) / (float)W;
     t.cy1 = ((float)(t.ty1 - 1) + 0.5f) / (float)H;
     t.pix = ((size_t)t.b * H + (t.valid ? t.y : 0)) * W + (t.valid ? t.x : 0);
-    t.tile = (((size_t)t.b * gridDim.y + t.by) * gridDim.x + t.bx) * WAVES + t.wave;
+    t.tile = (((size_t)t.b * gy + t.by) * gx + t.bx) * WAVES + t.wave;
     return t;
+}
+
+// Grid (gx, gy, B). With `perm` (setup_records' block order of B scenes)
+// launch slot i (the linear block index) works on block perm[s * nb + i / B]
+// of scene s = i % B.
+__device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int B = 1) {
+    const int gx = (int)gridDim.x, gy = (int)gridDim.y;
+    int b = (int)blockIdx.z, bx = (int)blockIdx.x, by = (int)blockIdx.y, rank = -1;
+    if (perm) {
+        const int nb = gx * gy;
+        const int i = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        b = i % B;
+        rank = i / B;
+        const int local = min(max(perm[(size_t)b * nb + rank], 0), nb - 1);
+        bx = local % gx;
+        by = local / gx;
+    }
+    return tile_at(W, H, gx, gy, b, bx, by, rank, 0, 1);
+}
+
+// The split backward's grid: B (nb + K (S - 1)) slots in one dimension. The
+// first B K S slots are the S segments of each scene's K heaviest blocks (by
+// setup_records' order), heaviest first, the rest one slot per remaining
+// block: slot i < B K S is segment (i / B) % S of rank i / (B S), later slots
+// segment 0 of rank K + (i - B K S) / B, of scene i % B.
+__device__ inline TileGeo tile_geo_split(int W, int H, int gx, int gy, const int* perm, int B, int S, int K) {
+    const int nb = gx * gy, i = (int)blockIdx.x, b = i % B;
+    int rank, seg = 0;
+    if (i < B * K * S) {
+        rank = i / (B * S);
+        seg = (i / B) % S;
+    } else {
+        rank = K + (i - B * K * S) / B;
+    }
+    const int local = min(max(perm[(size_t)b * nb + min(rank, nb - 1)], 0), nb - 1);
+    return tile_at(W, H, gx, gy, b, local % gx, local / gx, rank, seg, rank < K ? S : 1);
 }
 
 // Forward: composite in scene order (raster.rs:37-68). In the gradient modes it
@@ -831,7 +864,8 @@ __device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int 
 // register allocation; both kernels wait on scalar loads of the triangle
 // records once per list entry, and the extra waves hide that latency better
 // than the registers they cost would have saved (measured on B=16 256x256).
-template <int MODE, bool FAST>
+// CKPT: with the split backward's checkpoints (MODE_LOSS, MODE_GRAD_IN).
+template <int MODE, bool FAST, bool CKPT>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8))) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
     __shared__ uint32_t list[WAVES][CH];
     __shared__ double loss[WAVES];
@@ -856,6 +890,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     const int cap2 = a.cap2;
     // wave-uniform: the entry stores address from a scalar base
     TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
+    // Split backward: before recorded entry (c + 1) seg_m the pixel state goes to
+    // checkpoint c of this tile, the start of the backward's segment c + 1 (of
+    // the blocks the backward splits: those ranked below nsplit, or all
+    // without a block order here).
+    const bool split = CKPT && (tg.rank < 0 || tg.rank < a.nsplit);
+    const int nck = split ? max(a.nseg, 1) - 1 : 0;
+    int ck = 0, ck_at = nck > 0 ? a.seg_m : INT_MAX;
+    float* ckw = nck > 0 ? a.ckpt + (size_t)uniform_u32((uint32_t)tg.tile) * nck * (CKPT_WORDS * 64) : nullptr;
 
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
@@ -878,6 +920,18 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             // taped forward keeps (F_TAPE); in the other modes the two agree.
             const uint64_t tapedm = (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE)) ? onm : 0;
             const bool taped = __builtin_amdgcn_inverse_ballot_w64(tapedm);
+            if (CKPT && tapedm != 0 && n2 == ck_at) {
+                // the colour and transmittance with which the backward sweep reaches this entry
+                float* c = ckw + (size_t)ck * (CKPT_WORDS * 64) + lane;
+                c[0] = col[0];
+                c[64] = col[1];
+                c[128] = col[2];
+                c[192] = tot.q;
+                c[256] = __int_as_float(tot.z);
+                c[320] = __int_as_float(tot.e);
+                ck++;
+                ck_at = ck < nck ? ck_at + a.seg_m : INT_MAX;
+            }
             {
                 // raster.rs:60-66, kept only where the pair contributes, as
                 // col + w (c - col): one rounding fewer than c w + col (1 - w),
@@ -1082,12 +1136,33 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
     if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
+    // segments per tile: only the variant with neither rebuild nor fixed-order sums splits
+    const int S = (!REBUILD && !DET && a.perm_bwd) ? max(a.nseg, 1) : 1;
+    const TileGeo tg = S > 1 ? tile_geo_split(W, H, a.gx, a.gy, a.perm_bwd, a.B, S, a.nsplit)
+                             : tile_geo(W, H, a.perm_bwd, a.B);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
     const float rsig = 1.0f / sig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    const int n_chunks = (T + CH - 1) / CH;
+    const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
+    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
+    // This wave's entries: [i_begin, i_end) of the tile's recorded list.
+    int i_begin = 0, i_end = n2r;
+    if (tg.nseg > 1) {
+        i_begin = tg.seg * a.seg_m;
+        i_end = tg.seg == tg.nseg - 1 ? n2r : min(n2r, i_begin + a.seg_m);
+        if (tg.seg > 0) {
+            // the block (all of it, before any barrier) leaves when none of its
+            // four tiles has entries in this segment
+            const size_t t0 = tg.tile - (size_t)wave;
+            int most = 0;
+            for (int q = 0; q < WAVES; q++) most = max(most, (int)uniform_u32((uint32_t)a.tl_n[2 * (t0 + q)]));
+            if (most <= i_begin) return;
+        }
+    }
 
     Back st;
     {
@@ -1098,14 +1173,19 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
                                   : (MODE == MODE_LOSS ? ps.g0[ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
         }
     }
-    st.col[0] = a.bg[b * 3 + 0];
-    st.col[1] = a.bg[b * 3 + 1];
-    st.col[2] = a.bg[b * 3 + 2];
-    st.pre = {1.0f, 0, 0};
-
-    const int n_chunks = (T + CH - 1) / CH;
-    const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
-    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
+    if (i_begin > 0 && i_begin < n2r) {
+        // the forward kernel's checkpoint before entry i_begin
+        const float* c = a.ckpt + ((size_t)tg.tile * (a.nseg - 1) + (tg.seg - 1)) * (CKPT_WORDS * 64) + lane;
+        st.col[0] = c[0];
+        st.col[1] = c[64];
+        st.col[2] = c[128];
+        st.pre = {c[192], __float_as_int(c[256]), __float_as_int(c[320])};
+    } else {
+        st.col[0] = a.bg[b * 3 + 0];
+        st.col[1] = a.bg[b * 3 + 1];
+        st.col[2] = a.bg[b * 3 + 2];
+        st.pre = {1.0f, 0, 0};
+    }
     // wave-uniform, so the recorded entries are read with scalar loads
     const int cap2 = a.cap2;
     const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
@@ -1113,7 +1193,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     float* accw = acc[DET ? wave : 0];
     lds_float* const tw = (lds_float*)trans[wave];
     typedef __attribute__((address_space(3))) char lds_char;
-    int i2 = 0;
+    int i2 = i_begin;
     const bool plain = lane_mask(st.tot.z != 0 || st.tot.e != 0) == 0;
 
     // The entries the forward kernel recorded: which lanes contribute and
@@ -1122,7 +1202,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     auto recorded = [&](auto plain_c, int k0, int k1) {
         constexpr bool PLAIN = decltype(plain_c)::value;
         TileEnt nx = te[min(i2, cap2 - 1)];
-        for (; i2 < n2r; i2++) {
+        for (; i2 < i_end; i2++) {
             const TileEnt cur = nx;
             const int k = (int)(cur.k >> 8);
             if (k >= k1) break;
@@ -1214,8 +1294,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     }
     // The per-item loss (canvas.rs:45-58) from the forward kernel's per-block
     // sums, by the scene's first block, in a fixed order.
-    if (MODE == MODE_LOSS && !DET && tg.bx == 0 && tg.by == 0 && wave == 0) {
-        const int nblk = gridDim.x * gridDim.y;
+    if (MODE == MODE_LOSS && !DET && tg.bx == 0 && tg.by == 0 && tg.seg == 0 && wave == 0) {
+        // blocks per scene from the image size: the split grid is one-dimensional
+        const int nblk = ((W + 2 * TILE - 1) / (2 * TILE)) * ((H + 2 * TILE - 1) / (2 * TILE));
         const double* pl = a.partial_loss + (size_t)b * nblk;
         double l = 0.0;
         for (int r = lane; r < nblk; r += 64) l += pl[r];
@@ -1442,26 +1523,33 @@ dim3 raster_grid(int B, int W, int H) {
     return dim3((W + 2 * TILE - 1) / (2 * TILE), (H + 2 * TILE - 1) / (2 * TILE), B);
 }
 
-template <int MODE, bool FAST>
+template <int MODE, bool FAST, bool CKPT = false>
 static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((forward_kernel<MODE, FAST>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a, a.rec);
+    hipLaunchKernelGGL((forward_kernel<MODE, FAST, CKPT>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a,
+                       a.rec);
     return hipGetLastError();
+}
+
+template <int MODE, bool FAST>
+static hipError_t launch_forward_c(const RasterArgs& a, hipStream_t s) {
+    return (a.ckpt && a.nseg > 1) ? launch_forward_t<MODE, FAST, true>(a, s) : launch_forward_t<MODE, FAST, false>(a, s);
 }
 
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
     if (mode == MODE_RENDER)
         return fast ? launch_forward_t<MODE_RENDER, true>(a, s) : launch_forward_t<MODE_RENDER, false>(a, s);
     if (mode == MODE_LOSS)
-        return fast ? launch_forward_t<MODE_LOSS, true>(a, s) : launch_forward_t<MODE_LOSS, false>(a, s);
+        return fast ? launch_forward_c<MODE_LOSS, true>(a, s) : launch_forward_c<MODE_LOSS, false>(a, s);
     if (mode == MODE_RECORD)
         return fast ? launch_forward_t<MODE_RECORD, true>(a, s) : launch_forward_t<MODE_RECORD, false>(a, s);
-    return fast ? launch_forward_t<MODE_GRAD_IN, true>(a, s) : launch_forward_t<MODE_GRAD_IN, false>(a, s);
+    return fast ? launch_forward_c<MODE_GRAD_IN, true>(a, s) : launch_forward_c<MODE_GRAD_IN, false>(a, s);
 }
 
 template <int MODE, bool FAST, bool REBUILD, bool DET>
 static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD, DET>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0,
-                       s, a, a.rec, a.tl_ent);
+    const bool split = !REBUILD && !DET && a.perm_bwd && a.nseg > 1;
+    const dim3 grid = split ? dim3((unsigned)(a.B * (a.gx * a.gy + a.nsplit * (a.nseg - 1)))) : raster_grid(a.B, a.W, a.H);
+    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
     return hipGetLastError();
 }
 

@@ -53,6 +53,7 @@ enum Kind : uint64_t {
     K_RESIZE_U8,
     K_RESIZE_TAB,
     K_RESIZE_TMP,
+    K_CKPT,
 };
 
 // Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
@@ -225,7 +226,26 @@ struct RasterBufs {
     int* tn = nullptr;              // ntiles*2 (gradient modes)
     int* order = nullptr;           // B*nblk, or null: launch order
     int cap2 = 0;
+    float* ckpt = nullptr;          // split backward's checkpoints, or null: no split
+    int nseg = 1, seg_m = 0, nsplit = 0;  // its segments, entries per segment, split blocks per scene
 };
+
+// Split of the backward's sweep over a tile's recorded entries. A tile's sweep
+// is sequential, and the tiles with the longest lists sit together (a block's
+// four tiles are alike). A grid that does not fill the device (fewer blocks
+// than SPLIT_MAX_BLOCKS_PER_CU per compute unit) runs about one round of
+// blocks, so its heaviest blocks bound the backward kernel's time: there the
+// heaviest quarter of each scene's blocks by setup_records' estimate get
+// SPLIT_SEGMENTS waves per tile, each over ceil(T / SPLIT_DIVISOR) entries (the
+// last to the end), from checkpoints the forward kernel leaves. A grid of
+// several rounds is bound by throughput instead, and the split's extra blocks
+// and checkpoints only cost time there (measured: B=16 256x256 T=128). Used
+// with a block order, when gradients are summed with atomics and every entry
+// is recorded (the backward's variant with neither fixed-order sums nor the
+// rebuild path) and T is large enough for long lists; 1 (no split) otherwise.
+constexpr int SPLIT_SEGMENTS = 3, SPLIT_DIVISOR = 6, SPLIT_MIN_T = 48, SPLIT_BLOCK_SHARE = 4,
+              SPLIT_MAX_BLOCKS_PER_CU = 6;
+int backward_segments(int T, int cap2, bool det, size_t blocks, int cus);
 
 // The shared raster sequence over given buffers: records, the forward pass,
 // and (gradient modes) the backward pass and the partial-row reduction. With

@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -329,6 +330,12 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     a.perm_bwd = ord.perm;
     a.halt = halt;
+    a.nseg = bufs.ckpt && ord.perm ? bufs.nseg : 1;
+    a.seg_m = bufs.seg_m;
+    a.nsplit = bufs.nsplit;
+    a.gx = (int)grid.x;
+    a.gy = (int)grid.y;
+    a.ckpt = bufs.ckpt;
     {
         KernelTimer kt(ctx, TK_RASTER, s, timed);
         HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
@@ -346,6 +353,11 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     return DRH_OK;
 }
 
+int backward_segments(int T, int cap2, bool det, size_t blocks, int cus) {
+    if (det || cap2 < T || T < SPLIT_MIN_T || blocks >= (size_t)SPLIT_MAX_BLOCKS_PER_CU * (size_t)cus) return 1;
+    return SPLIT_SEGMENTS;
+}
+
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
                int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
                hipStream_t s, const int* halt) {
@@ -353,7 +365,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
     const size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pstate, tent, tn, order;
+    Lease rec, partials, ploss, pstate, tent, tn, order, ckpt;
     RasterBufs bufs;
     bufs.cap2 = tile_entries(ntiles, T);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
@@ -369,6 +381,15 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
         if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
         bufs.order = order.get<int>();
+        const int nseg = mode == drh::MODE_RENDER ? 1 : backward_segments(T, bufs.cap2, det, (size_t)B * nblk, ctx->cus);
+        if (nseg > 1) {
+            const size_t words = ntiles * (size_t)(nseg - 1) * drh::CKPT_WORDS * 64;
+            if ((rc = ckpt.acquire(ctx, K_CKPT, words * sizeof(float), s))) return rc;
+            bufs.ckpt = ckpt.get<float>();
+            bufs.nseg = nseg;
+            bufs.seg_m = (T + SPLIT_DIVISOR - 1) / SPLIT_DIVISOR;
+            bufs.nsplit = std::max(1, nblk / SPLIT_BLOCK_SHARE);
+        }
     }
     bufs.rec = rec.get<float>();
     bufs.partials = partials.get<float>();

@@ -83,6 +83,33 @@ def test_backward_from_grad_matches_oracle(ctx, orc, name, B, H, W, T, sigma, ki
     assert_grads(gpu, inv, label=f"{name} inverted")
 
 
+@pytest.mark.parametrize("mode", ["loss", "from_grad"])
+def test_split_backward_matches_oracle(ctx, orc, mode):
+    # Six 128x128 scenes of large triangles: 384 blocks, under six per compute
+    # unit, so the backward splits the sweep of the heaviest quarter of blocks
+    # over three waves per tile from the forward kernel's checkpoints (tiles
+    # with up to ~60 recorded entries). Against the oracle, and against the
+    # fixed-order mode, which never splits.
+    B, H, W, T, sigma = 6, 128, 128, 128, 0.0015
+    params = synth.batch("uniform", B, T, 41)
+    bgs = synth.uniforms(47, B * 3).reshape(B, 3).astype(np.float32)
+    print(f"split backward {mode}", flush=True)
+    if mode == "loss":
+        targets = orc.render_batch(synth.batch("uniform", B, T, 41, target_offset=1000), H, W, sigma, bgs[::-1].copy())
+        gl, gg = ctx.fused_loss_backward(params, targets, sigma, bgs)
+        dl, dg = ctx.fused_loss_backward(params, targets, sigma, bgs, deterministic=True)
+        cl, cg = orc.loss_backward_batch(params, targets, sigma, bgs)
+        check_losses(gl, cl)
+        assert np.array_equal(gl, dl)
+    else:
+        gin = ((synth.uniforms(49, B * H * W * 3) - 0.5) * 1e-3).reshape(B, H, W, 3).astype(np.float32)
+        gg = ctx.backward_from_grad(params, gin, sigma, bgs)
+        dg = ctx.backward_from_grad(params, gin, sigma, bgs, deterministic=True)
+        cg = orc.backward_from_grad_batch(params, gin, sigma, bgs)
+    assert_grads(gg, cg, label=f"split {mode}")
+    assert grad_err(gg, dg) <= 1e-6
+
+
 def test_opaque_stack_and_clamped_alpha(ctx, orc):
     # alpha >= 1 makes w == 1 exactly deep inside: zero transmittance factors.
     params = synth.batch("uniform", 2, 20, 9)
