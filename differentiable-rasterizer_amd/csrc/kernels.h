@@ -67,12 +67,16 @@ struct TileEnt {
 };
 static_assert(sizeof(TileEnt) == 24, "TileEnt is read as 2 + 4 dwords");
 
-// Per-pixel state the forward kernel hands to the backward kernel.
-struct PixState {
-    float g0[3];  // dL/dpixel (MODE_LOSS; MODE_GRAD_IN reads the caller's)
-    float q;      // total transmittance: product of the nonzero (1 - w),
-    int z, e;     // the count of zero factors and of 2^64 rescalings of q
-};
+// Per-pixel state the forward kernel hands to the backward kernel, field-major:
+//   q   B*H*W floats: the pixel's total transmittance, the product of its
+//       nonzero (1 - w) factors, kept in [2^-64, 1];
+//   g0  B*H*W*3 floats: dL/dpixel (MODE_LOSS; MODE_GRAD_IN reads the caller's);
+//   ze  per tile and lane: the count of zero factors and of 2^64 rescalings of
+//       q, written only for a tile where some lane has either (TN_IRREGULAR set
+//       in its tl_n[2 tile + 1]); zero for every other tile.
+// 16 bytes per pixel in MODE_LOSS and 4 otherwise, against 24 with all five
+// words per pixel: the counts are zero for nearly every pixel.
+constexpr int TN_IRREGULAR = 1 << 30;
 
 // The raster kernels' block order, made by setup_records (perm null: none):
 // perm[b * gx*gy + r] is the scene-local index of scene b's r-th heaviest block;
@@ -93,10 +97,12 @@ struct RasterArgs {
     float* out_img;        // B*H*W*3 (MODE_RENDER, MODE_RECORD; optional in MODE_LOSS)
     float* partials;       // B*nblk*T*NP
     double* partial_loss;  // B*nblk
-    PixState* pstate;      // B*H*W
+    float* pq;             // B*H*W total transmittance
+    float* pg0;            // B*H*W*3 dL/dpixel (MODE_LOSS)
+    int2* pze;             // ntiles*64 zero and rescaling counts (irregular tiles)
     TileEnt* tl_ent;       // ntiles*cap2 recorded entries
     int cap2;              // entries recorded per tile
-    int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded
+    int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded | TN_IRREGULAR
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)
     int deterministic;     // per-block partial rows + reduce_partials instead of atomics

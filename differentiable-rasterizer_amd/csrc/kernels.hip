@@ -980,15 +980,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     }
     if (MODE == MODE_RENDER) return;
 
+    // the counts only where some lane of the tile has any (TN_IRREGULAR)
+    const bool irregular = lane_mask(tot.z != 0 || tot.e != 0) != 0;
     if (lane == 0) {
         a.tl_n[2 * tg.tile] = min(n2, cap2);
-        a.tl_n[2 * tg.tile + 1] = rec_chunks;
+        a.tl_n[2 * tg.tile + 1] = rec_chunks | (irregular ? TN_IRREGULAR : 0);
     }
-    PixState ps;
-    ps.g0[0] = ps.g0[1] = ps.g0[2] = 0.0f;
-    ps.q = tot.q;
-    ps.z = tot.z;
-    ps.e = tot.e;
+    if (irregular) a.pze[tg.tile * 64 + lane] = make_int2(tot.z, tot.e);
+    if (tg.valid) a.pq[tg.pix] = tot.q;
     if (MODE == MODE_LOSS) {
         double l = 0.0;
         if (tg.valid) {
@@ -997,7 +996,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
                 float t = a.target[img_index(a, tg.pix, b, ch)];
                 float d = col[ch] - t;
                 l += (double)d * (double)d;
-                ps.g0[ch] = scale * (col[ch] - t);
+                a.pg0[tg.pix * 3 + ch] = scale * (col[ch] - t);
             }
         }
         l = wave_sum_f64(l);
@@ -1009,7 +1008,6 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
             a.partial_loss[tg.tile / WAVES] = lb;
         }
     }
-    if (tg.valid) a.pstate[tg.pix] = ps;
 }
 
 // Per-pixel state of the backward sweep.
@@ -1148,7 +1146,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
 
     const int n_chunks = (T + CH - 1) / CH;
     const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
-    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]);
+    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]) & ~TN_IRREGULAR;
     // This wave's entries: [i_begin, i_end) of the tile's recorded list.
     int i_begin = 0, i_end = n2r;
     if (tg.nseg > 1) {
@@ -1165,12 +1163,14 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     }
 
     Back st;
+    const bool irregular = (a.tl_n[2 * tg.tile + 1] & TN_IRREGULAR) != 0;  // wave-uniform
     {
-        PixState ps = a.pstate[tg.pix];
-        st.tot = {ps.q, ps.z, ps.e};
+        int2 ze = make_int2(0, 0);
+        if (irregular) ze = a.pze[tg.tile * 64 + lane];
+        st.tot = {a.pq[tg.pix], ze.x, ze.y};
         for (int ch = 0; ch < 3; ch++) {
             st.g0[ch] = !tg.valid ? 0.0f
-                                  : (MODE == MODE_LOSS ? ps.g0[ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
+                                  : (MODE == MODE_LOSS ? a.pg0[tg.pix * 3 + ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
         }
     }
     if (i_begin > 0 && i_begin < n2r) {
@@ -1194,7 +1194,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     lds_float* const tw = (lds_float*)trans[wave];
     typedef __attribute__((address_space(3))) char lds_char;
     int i2 = i_begin;
-    const bool plain = lane_mask(st.tot.z != 0 || st.tot.e != 0) == 0;
+    // no lane of the tile met a zero factor or a rescaling in the forward pass
+    const bool plain = !irregular;
 
     // The entries the forward kernel recorded: which lanes contribute and
     // which of them took the exact path are known; only w is recomputed. The

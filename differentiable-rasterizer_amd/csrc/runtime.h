@@ -44,6 +44,8 @@ enum Kind : uint64_t {
     K_FIT_F32,
     K_FIT_STATE,
     K_PIXSTATE,
+    K_PIX_G0,
+    K_PIX_ZE,
     K_TILE_ENT,
     K_TILE_N,
     K_SRGB_F32,
@@ -221,7 +223,9 @@ struct RasterBufs {
     float* rec = nullptr;           // B*T*REC
     float* partials = nullptr;      // B*nblk*T*NP (deterministic gradient modes)
     double* ploss = nullptr;        // B*nblk (gradient modes)
-    drh::PixState* pstate = nullptr;  // B*H*W (gradient modes)
+    float* pq = nullptr;            // B*H*W (gradient modes)
+    float* pg0 = nullptr;           // B*H*W*3 (MODE_LOSS)
+    int2* pze = nullptr;            // ntiles*64 (gradient modes)
     drh::TileEnt* tent = nullptr;   // ntiles*cap2 (gradient modes)
     int* tn = nullptr;              // ntiles*2 (gradient modes)
     int* order = nullptr;           // B*nblk, or null: launch order

@@ -319,7 +319,9 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.out_img = out_img;
     a.partials = bufs.partials;
     a.partial_loss = bufs.ploss;
-    a.pstate = bufs.pstate;
+    a.pq = bufs.pq;
+    a.pg0 = bufs.pg0;
+    a.pze = bufs.pze;
     a.tl_ent = bufs.tent;
     a.cap2 = bufs.cap2;
     a.tl_n = bufs.tn;
@@ -365,7 +367,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
     const size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pstate, tent, tn, order, ckpt;
+    Lease rec, partials, ploss, pq, pg0, pze, tent, tn, order, ckpt;
     RasterBufs bufs;
     bufs.cap2 = tile_entries(ntiles, T);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
@@ -374,7 +376,10 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
             return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
-        if ((rc = pstate.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(drh::PixState), s))) return rc;
+        if ((rc = pq.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(float), s))) return rc;
+        if (mode == drh::MODE_LOSS && (rc = pg0.acquire(ctx, K_PIX_G0, (size_t)B * H * W * 3 * sizeof(float), s)))
+            return rc;
+        if ((rc = pze.acquire(ctx, K_PIX_ZE, ntiles * 64 * sizeof(int2), s))) return rc;
         if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
         if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
     }
@@ -394,7 +399,9 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     bufs.rec = rec.get<float>();
     bufs.partials = partials.get<float>();
     bufs.ploss = ploss.get<double>();
-    bufs.pstate = pstate.get<drh::PixState>();
+    bufs.pq = pq.get<float>();
+    bufs.pg0 = pg0.get<float>();
+    bufs.pze = pze.get<int2>();
     bufs.tent = tent.get<drh::TileEnt>();
     bufs.tn = tn.get<int>();
     return run_raster_bufs(ctx, mode, params, bgs, img_in, B, T, H, W, sigma, out_img, out_grads, out_losses, flags,
@@ -409,11 +416,12 @@ using namespace drh_rt;
 
 // The forward record that drh_render_record leaves for drh_backward_recorded,
 // in device memory the caller owns: a head (sizes, sigma, math mode), the
-// triangle records, a copy of the backgrounds, the per-pixel hand-over, the
-// per-tile entries (with their counts) and the backward kernel's block order,
-// each starting at a 256-byte boundary.
+// triangle records, a copy of the backgrounds, the per-pixel hand-over (total
+// transmittance, and the zero and rescaling counts of the tiles that have
+// any), the per-tile entries (with their counts) and the backward kernel's
+// block order, each starting at a 256-byte boundary.
 struct RecordLayout {
-    size_t head = 0, rec = 0, bg = 0, pstate = 0, tl_n = 0, tl_ent = 0, ord = 0, total = 0;
+    size_t head = 0, rec = 0, bg = 0, pq = 0, pze = 0, tl_n = 0, tl_ent = 0, ord = 0, total = 0;
     int cap2 = 0;
 };
 
@@ -431,8 +439,10 @@ RecordLayout record_layout(int64_t B, int64_t T, int64_t H, int64_t W) {
     off = up(off + (size_t)B * T * drh::REC * sizeof(float));
     L.bg = off;
     off = up(off + (size_t)B * 3 * sizeof(float));
-    L.pstate = off;
-    off = up(off + (size_t)B * H * W * sizeof(drh::PixState));
+    L.pq = off;
+    off = up(off + (size_t)B * H * W * sizeof(float));
+    L.pze = off;
+    off = up(off + ntiles * 64 * sizeof(int2));
     L.tl_n = off;
     off = up(off + ntiles * 2 * sizeof(int));
     L.tl_ent = off;
@@ -806,7 +816,8 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     a.rec = reinterpret_cast<float*>(base + L.rec);
     a.bg = reinterpret_cast<float*>(base + L.bg);
     a.out_img = img.dev;
-    a.pstate = reinterpret_cast<drh::PixState*>(base + L.pstate);
+    a.pq = reinterpret_cast<float*>(base + L.pq);
+    a.pze = reinterpret_cast<int2*>(base + L.pze);
     a.tl_ent = reinterpret_cast<drh::TileEnt*>(base + L.tl_ent);
     a.cap2 = L.cap2;
     a.tl_n = reinterpret_cast<int*>(base + L.tl_n);
@@ -866,7 +877,8 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     a.grad_in = gi.dev;
     a.partials = partials.get<float>();
     // read only by the backward kernel; the casts follow RasterArgs' field types
-    a.pstate = reinterpret_cast<drh::PixState*>(const_cast<char*>(base + L.pstate));
+    a.pq = reinterpret_cast<float*>(const_cast<char*>(base + L.pq));
+    a.pze = reinterpret_cast<int2*>(const_cast<char*>(base + L.pze));
     a.tl_ent = reinterpret_cast<drh::TileEnt*>(const_cast<char*>(base + L.tl_ent));
     a.cap2 = L.cap2;
     a.tl_n = reinterpret_cast<int*>(const_cast<char*>(base + L.tl_n));

@@ -41,7 +41,7 @@ void* scratch_addr(int device) {
 // tile when they fit, else fewer, and tiles past them rebuild their lists in
 // the backward kernel).
 struct ScratchLayout {
-    size_t rec = 0, ploss = 0, pstate = 0, tn = 0, order = 0, partials = 0, tent = 0, total = 0;
+    size_t rec = 0, ploss = 0, pq = 0, pg0 = 0, pze = 0, tn = 0, order = 0, partials = 0, tent = 0, total = 0;
     int cap2 = 0;
     bool ordered = false;
 };
@@ -56,8 +56,12 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     off = up(off + (size_t)B * T * drh::REC * sizeof(float));
     L.ploss = off;
     off = up(off + (size_t)B * nblk * sizeof(double));
-    L.pstate = off;
-    off = up(off + (size_t)B * H * W * sizeof(drh::PixState));
+    L.pq = off;
+    off = up(off + (size_t)B * H * W * sizeof(float));
+    L.pg0 = off;
+    off = up(off + (size_t)B * H * W * 3 * sizeof(float));
+    L.pze = off;
+    off = up(off + ntiles * 64 * sizeof(int2));
     L.tn = off;
     off = up(off + ntiles * 2 * sizeof(int));
     L.ordered = use_order(ctx, B, (int)grid.x, (int)grid.y);
@@ -116,7 +120,9 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
     RasterBufs bufs;
     bufs.rec = reinterpret_cast<float*>(base + L.rec);
     bufs.ploss = reinterpret_cast<double*>(base + L.ploss);
-    bufs.pstate = reinterpret_cast<drh::PixState*>(base + L.pstate);
+    bufs.pq = reinterpret_cast<float*>(base + L.pq);
+    bufs.pg0 = reinterpret_cast<float*>(base + L.pg0);
+    bufs.pze = reinterpret_cast<int2*>(base + L.pze);
     bufs.tn = reinterpret_cast<int*>(base + L.tn);
     bufs.order = L.ordered ? reinterpret_cast<int*>(base + L.order) : nullptr;
     bufs.partials = det ? reinterpret_cast<float*>(base + L.partials) : nullptr;

@@ -75,21 +75,24 @@ def test_create_reports_no_device_without_a_gpu(L):
 
 def test_record_bytes_cover_every_part(L):
     # host-only sizing of the forward record: triangle records (76 floats each),
-    # backgrounds, 24 bytes per pixel, two counts per tile, T entries of 24 bytes
-    # per 8x8 tile, and the block order (one int per 16x16 block), each part
-    # rounded up to 256 bytes
+    # backgrounds, the transmittance (4 bytes per pixel), room for the zero and
+    # rescaling counts of every tile lane (8 bytes each, written only for tiles
+    # that have any), two counts per tile, T entries of 24 bytes per 8x8 tile,
+    # and the block order (one int per 16x16 block), each part rounded up to 256
+    # bytes
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     B, T, H, W = 16, 128, 256, 256
     tiles = B * (W // 8) * (H // 8)
     head = 256  # sizes, sigma and math mode of the forward pass
-    want = (head + up(B * T * 76 * 4) + up(B * 3 * 4) + up(B * H * W * 24) + up(tiles * 8) + up(tiles * T * 24)
-            + up(tiles // 4 * 4))
+    want = (head + up(B * T * 76 * 4) + up(B * 3 * 4) + up(B * H * W * 4) + up(tiles * 64 * 8) + up(tiles * 8)
+            + up(tiles * T * 24) + up(tiles // 4 * 4))
     assert L.record_bytes(B, T, H, W) == want
     assert L.record_bytes(0, T, H, W) == 0
     # odd sizes count the partial tiles of whole 16x16 blocks
     tiles = 3 * 2 * 2 * 4  # 2 x 2 blocks of 2 x 2 tiles per scene
-    assert L.record_bytes(3, 5, 17, 30) == (head + up(3 * 5 * 76 * 4) + up(36) + up(3 * 17 * 30 * 24)
-                                           + up(tiles * 8) + up(tiles * 5 * 24) + up(tiles // 4 * 4))
+    assert L.record_bytes(3, 5, 17, 30) == (head + up(3 * 5 * 76 * 4) + up(36) + up(3 * 17 * 30 * 4)
+                                           + up(tiles * 64 * 8) + up(tiles * 8) + up(tiles * 5 * 24)
+                                           + up(tiles // 4 * 4))
     with pytest.raises(L.DiffrastError) as e:
         L.record_bytes(1, 1, 0, 4)
     assert e.value.code == 6
@@ -102,6 +105,6 @@ def test_record_keeps_a_bounded_number_of_entries(L, monkeypatch):
     cap = (1 << 30) // (tiles * 24)
     assert cap >= 128
     n = L.record_bytes(B, T, H, W)
-    assert n - (1 << 30) < B * T * 76 * 4 + B * H * W * 24 + tiles * 8 + tiles // 4 * 4 + 4096
+    assert n - (1 << 30) < B * T * 76 * 4 + B * H * W * 4 + tiles * 64 * 8 + tiles * 8 + tiles // 4 * 4 + 4096
     monkeypatch.setenv("DRH_MAX_TILE_ENTRIES", "7")
     assert L.record_bytes(2, 50, 16, 16) < L.record_bytes(2, 7, 16, 16) + 2 * 50 * 76 * 4
