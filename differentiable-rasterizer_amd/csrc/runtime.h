@@ -58,9 +58,13 @@ enum Kind : uint64_t {
     K_CKPT,
 };
 
-// Bytes the pool keeps (crates/diffrast-gpu/src/lib.rs:123-130); buffers
-// released beyond it are freed.
+// Bytes the pool keeps at least (crates/diffrast-gpu/src/lib.rs:123-130);
+// buffers released beyond a context's limit are freed. The reference's 512 MiB
+// suits a 24 GB card; a context keeps max(512 MiB, 1/32 of the device's memory)
+// (9 GB on a 288 GB MI355X), so that batches of 64 scenes at 256x256 reuse
+// their buffers instead of freeing them (a stream wait) on every call.
 constexpr uint64_t POOL_BYTE_LIMIT = 512ull << 20;
+constexpr uint64_t POOL_MEMORY_SHARE = 32;
 
 struct PoolBuf {
     void* ptr = nullptr;
@@ -87,6 +91,7 @@ struct drh_ctx {
     std::mutex mu;
     std::unordered_map<uint64_t, std::vector<drh_rt::PoolBuf>> free_bufs;
     uint64_t hits = 0, misses = 0, bytes = 0;
+    uint64_t pool_limit = drh_rt::POOL_BYTE_LIMIT;  // bytes the pool keeps (set by drh_create)
     // Set once buffers have been used on more than one stream. Until then
     // every use of a buffer is ordered by the one stream and releases record
     // no event (an event record costs a GPU-side marker per buffer per call).

@@ -96,7 +96,7 @@ void Lease::release() {
     bool keep = false;
     {
         std::lock_guard<std::mutex> g(ctx_->mu);
-        if (ctx_->bytes + buf_.bytes <= POOL_BYTE_LIMIT) {
+        if (ctx_->bytes + buf_.bytes <= ctx_->pool_limit) {
             ctx_->bytes += buf_.bytes;
             ctx_->free_bufs[pool_key(kind_, buf_.bytes)].push_back(buf_);
             keep = true;
@@ -593,6 +593,7 @@ int drh_create(drh_ctx** out) {
     c->device = dev;
     c->discrete = prop.integrated == 0;
     c->cus = prop.multiProcessorCount;
+    c->pool_limit = std::max<uint64_t>(POOL_BYTE_LIMIT, (uint64_t)prop.totalGlobalMem / POOL_MEMORY_SHARE);
     char buf[512];
     std::snprintf(buf, sizeof buf, "%s (%s, %d CUs, HIP)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
     c->info = buf;
