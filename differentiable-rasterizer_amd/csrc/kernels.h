@@ -165,6 +165,12 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
 hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s);
+// Forward and backward of a gradient mode in one kernel (hipErrorInvalidValue
+// unless cap2 >= T, cap2 % 8 == 0, not deterministic, no split); in MODE_LOSS
+// launch_sum_losses then forms the per-scene losses from its per-block partials.
+hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s);
+hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, double npix3, float* losses, hipStream_t s,
+                             const int* halt = nullptr);
 // npix3: 3 H W, the divisor of the per-item loss (canvas.rs:45-58)
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
                          double npix3, float* grads, float* losses, hipStream_t s, const int* halt = nullptr);

@@ -865,28 +865,20 @@ __device__ inline TileGeo tile_geo_split(int W, int H, int gx, int gy, const int
 // records once per list entry, and the extra waves hide that latency better
 // than the registers they cost would have saved (measured on B=16 256x256).
 // CKPT: with the split backward's checkpoints (MODE_LOSS, MODE_GRAD_IN).
+// The forward sweep of one tile (raster.rs:37-68): composites its pixels over
+// every chunk of triangles into col (which comes in as the background) and, in
+// the gradient modes, multiplies the taped transmittance into tot (which comes
+// in as an empty product) and records the tile's contributing entries: n2 of
+// them seen, those of the first rec_chunks chunks all recorded. With CKPT, the
+// split backward's checkpoints too. lw: the wave's LDS list.
 template <int MODE, bool FAST, bool CKPT>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8))) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
-    __shared__ uint32_t list[WAVES][CH];
-    __shared__ double loss[WAVES];
-    if (a.halt && *a.halt >= 0) return;
-    const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
-    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
-    const int lane = tg.lane, wave = tg.wave, b = tg.b;
-    const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
-    const float* __restrict__ rec = records + (size_t)b * T * REC;
-
-    float col[3];
-    col[0] = a.bg[b * 3 + 0];
-    col[1] = a.bg[b * 3 + 1];
-    col[2] = a.bg[b * 3 + 2];
-    Trans tot = {1.0f, 0, 0};
-
+__device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* __restrict__ rec, const TileGeo& tg,
+                                              uint64_t validm, float rsig, float sig, uint32_t* lw,
+                                              float (&col)[3], Trans& tot, int& n2, int& rec_chunks) {
+    const int T = a.T, lane = tg.lane;
     const int n_chunks = (T + CH - 1) / CH;
-    int n2 = 0;                 // contributing entries seen (recorded while n2 < cap2)
-    int rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
+    n2 = 0;                 // contributing entries seen (recorded while n2 < cap2)
+    rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
     const int cap2 = a.cap2;
     // wave-uniform: the entry stores address from a scalar base
     TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
@@ -902,12 +894,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     for (int c = 0; c < n_chunks; c++) {
         int k0 = c * CH, k1 = min(T, k0 + CH);
         int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0, tg.cx1,
-                                         tg.cy1, list[wave], lane, F_LIVE)
+                                         tg.cy1, lw, lane, F_LIVE)
                             : 0;
-        uint32_t nxt = list[wave][0];  // the next entry is read one iteration ahead
+        uint32_t nxt = lw[0];  // the next entry is read one iteration ahead
         for (int i = 0; i < count; i++) {
             const uint32_t ent = uniform_u32(nxt);
-            nxt = list[wave][min(i + 1, CH - 1)];
+            nxt = lw[min(i + 1, CH - 1)];
             const int k = k0 + (int)(ent >> 8);
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
@@ -970,6 +962,29 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
         }
         if (n2 > cap2 && rec_chunks == n_chunks) rec_chunks = c;
     }
+}
+
+template <int MODE, bool FAST, bool CKPT>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8))) void forward_kernel(RasterArgs a, const float* __restrict__ records) {
+    __shared__ uint32_t list[WAVES][CH];
+    __shared__ double loss[WAVES];
+    if (a.halt && *a.halt >= 0) return;
+    const int W = a.W, H = a.H, T = a.T;
+    const TileGeo tg = tile_geo(W, H, a.perm_fwd, a.B);
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
+    const int lane = tg.lane, wave = tg.wave, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = 1.0f / sig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    float col[3];
+    col[0] = a.bg[b * 3 + 0];
+    col[1] = a.bg[b * 3 + 1];
+    col[2] = a.bg[b * 3 + 2];
+    Trans tot = {1.0f, 0, 0};
+    int n2, rec_chunks;
+    forward_sweep<MODE, FAST, CKPT>(a, rec, tg, validm, rsig, sig, list[wave], col, tot, n2, rec_chunks);
+    const int cap2 = a.cap2;
 
     if (MODE == MODE_RENDER || MODE == MODE_RECORD || (MODE == MODE_LOSS && a.out_img)) {
         if (tg.valid) {
@@ -1112,90 +1127,29 @@ __device__ inline void reduce_entry(const float (&a)[NP], lds_float* tw, lds_flo
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
-// forward kernel recorded, again in scene order. The gradient reaching layer
-// k, d_canvas * prod_{j>k} (1 - w_j) (grad.rs:162-169), is formed as a ratio
-// of transmittance products instead of being peeled off a tape. Per-triangle
-// gradients are wave-reduced, accumulated per wave in LDS and written as one
-// partial row per block and chunk.
-// REBUILD: with the rebuild path for tiles past the recorded entries. Without
-// it (the entries cover T, the usual case) the kernel needs ~55 VGPRs instead
-// of ~95, so it runs uncapped.
-// DET: deterministic mode. Each wave adds into its own accumulator rows and the
-// block sums them in wave order; otherwise the four waves share one set of
-// rows (adds from different waves land in any order, as the float atomics
-// into the output do anyway) and the block needs a quarter of the LDS.
+// The backward sweep of one tile (grad.rs:135-182) over its recorded entries
+// [i_begin, i_end) and, with REBUILD, the chunks from rec_chunks on rebuilt and
+// classified again; the block's sums go out per chunk (atomics, or partial rows
+// with DET). st: the pixel state at entry i_begin; plain: no lane of the tile
+// met a zero factor or a rescaling in the forward pass. lw: the wave's LDS
+// list; acc: ROWS x CH x NP accumulators; trans: WAVES x NP x TP.
 template <int MODE, bool FAST, bool REBUILD, bool DET>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? (DET ? 4 : 6) : (DET ? 5 : 7)))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
-                                                               const TileEnt* __restrict__ ents) {
+__device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float* __restrict__ rec,
+                                               const TileEnt* __restrict__ ents, const TileGeo& tg,
+                                               uint64_t validm, float rsig, float sig, Back& st, int i_begin,
+                                               int i_end, int rec_chunks, bool plain, uint32_t* lw, float* acc,
+                                               float* trans) {
     constexpr int ROWS = DET ? WAVES : 1;  // accumulator row sets
-    __shared__ uint32_t list[WAVES][CH];
-    __shared__ __attribute__((aligned(16))) float acc[ROWS][CH * NP];
-    __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
-    if (a.halt && *a.halt >= 0) return;
-    const int W = a.W, H = a.H, T = a.T;
-    // segments per tile: only the variant with neither rebuild nor fixed-order sums splits
-    const int S = (!REBUILD && !DET && a.perm_bwd) ? max(a.nseg, 1) : 1;
-    const TileGeo tg = S > 1 ? tile_geo_split(W, H, a.gx, a.gy, a.perm_bwd, a.B, S, a.nsplit)
-                             : tile_geo(W, H, a.perm_bwd, a.B);
-    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
-    const int lane = tg.lane, wave = tg.wave, b = tg.b;
-    const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
-    const float* __restrict__ rec = records + (size_t)b * T * REC;
-
+    const int T = a.T, lane = tg.lane, wave = tg.wave, b = tg.b;
     const int n_chunks = (T + CH - 1) / CH;
-    const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
-    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]) & ~TN_IRREGULAR;
-    // This wave's entries: [i_begin, i_end) of the tile's recorded list.
-    int i_begin = 0, i_end = n2r;
-    if (tg.nseg > 1) {
-        i_begin = tg.seg * a.seg_m;
-        i_end = tg.seg == tg.nseg - 1 ? n2r : min(n2r, i_begin + a.seg_m);
-        if (tg.seg > 0) {
-            // the block (all of it, before any barrier) leaves when none of its
-            // four tiles has entries in this segment
-            const size_t t0 = tg.tile - (size_t)wave;
-            int most = 0;
-            for (int q = 0; q < WAVES; q++) most = max(most, (int)uniform_u32((uint32_t)a.tl_n[2 * (t0 + q)]));
-            if (most <= i_begin) return;
-        }
-    }
-
-    Back st;
-    const bool irregular = (a.tl_n[2 * tg.tile + 1] & TN_IRREGULAR) != 0;  // wave-uniform
-    {
-        int2 ze = make_int2(0, 0);
-        if (irregular) ze = a.pze[tg.tile * 64 + lane];
-        st.tot = {a.pq[tg.pix], ze.x, ze.y};
-        for (int ch = 0; ch < 3; ch++) {
-            st.g0[ch] = !tg.valid ? 0.0f
-                                  : (MODE == MODE_LOSS ? a.pg0[tg.pix * 3 + ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
-        }
-    }
-    if (i_begin > 0 && i_begin < n2r) {
-        // the forward kernel's checkpoint before entry i_begin
-        const float* c = a.ckpt + ((size_t)tg.tile * (a.nseg - 1) + (tg.seg - 1)) * (CKPT_WORDS * 64) + lane;
-        st.col[0] = c[0];
-        st.col[1] = c[64];
-        st.col[2] = c[128];
-        st.pre = {c[192], __float_as_int(c[256]), __float_as_int(c[320])};
-    } else {
-        st.col[0] = a.bg[b * 3 + 0];
-        st.col[1] = a.bg[b * 3 + 1];
-        st.col[2] = a.bg[b * 3 + 2];
-        st.pre = {1.0f, 0, 0};
-    }
     // wave-uniform, so the recorded entries are read with scalar loads
     const int cap2 = a.cap2;
     const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
     const size_t blk = tg.tile / WAVES;
-    float* accw = acc[DET ? wave : 0];
-    lds_float* const tw = (lds_float*)trans[wave];
+    float* accw = acc + (DET ? wave : 0) * (CH * NP);
+    lds_float* const tw = (lds_float*)(trans + wave * (NP * TP));
     typedef __attribute__((address_space(3))) char lds_char;
     int i2 = i_begin;
-    // no lane of the tile met a zero factor or a rescaling in the forward pass
-    const bool plain = !irregular;
 
     // The entries the forward kernel recorded: which lanes contribute and
     // which of them took the exact path are known; only w is recomputed. The
@@ -1251,10 +1205,10 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
             // Fallback when the forward kernel ran out of record space: rebuild
             // the chunk's list and classify every pair again.
             int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
-                                             tg.cx1, tg.cy1, list[wave], lane, F_TAPE)
+                                             tg.cx1, tg.cy1, lw, lane, F_TAPE)
                                 : 0;
             for (int i = 0; i < count; i++) {
-                const uint32_t ent = uniform_u32(list[wave][i]);
+                const uint32_t ent = uniform_u32(lw[i]);
                 const int kl = (int)(ent >> 8);
                 const float* rp = rec + (size_t)(k0 + kl) * REC;
                 const Rec r = load_rec(rp);
@@ -1280,19 +1234,97 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
         if (DET) {
             float* prow = a.partials + (blk * T + k0) * NP;
             for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
-                float v = acc[0][j];
-                for (int q = 1; q < ROWS; q++) v += acc[q][j];
+                float v = acc[j];
+                for (int q = 1; q < ROWS; q++) v += acc[q * (CH * NP) + j];
                 prow[j] = v;
             }
         } else {
             float* grow = a.grads + ((size_t)b * T + k0) * NP;
             for (int j = threadIdx.x; j < nk * NP; j += WAVES * 64) {
-                const float v = acc[0][j];
+                const float v = acc[j];
                 if (v != 0.0f) unsafeAtomicAdd(grow + j, v);
             }
         }
         __syncthreads();
     }
+}
+
+// Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
+// forward kernel recorded, again in scene order. The gradient reaching layer
+// k, d_canvas * prod_{j>k} (1 - w_j) (grad.rs:162-169), is formed as a ratio
+// of transmittance products instead of being peeled off a tape. Per-triangle
+// gradients are wave-reduced, accumulated per wave in LDS and written as one
+// partial row per block and chunk.
+// REBUILD: with the rebuild path for tiles past the recorded entries. Without
+// it (the entries cover T, the usual case) the kernel needs ~55 VGPRs instead
+// of ~95, so it runs uncapped.
+// DET: deterministic mode. Each wave adds into its own accumulator rows and the
+// block sums them in wave order; otherwise the four waves share one set of
+// rows (adds from different waves land in any order, as the float atomics
+// into the output do anyway) and the block needs a quarter of the LDS.
+template <int MODE, bool FAST, bool REBUILD, bool DET>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBUILD ? (DET ? 4 : 6) : (DET ? 5 : 7)))) void backward_kernel(RasterArgs a, const float* __restrict__ records,
+                                                               const TileEnt* __restrict__ ents) {
+    constexpr int ROWS = DET ? WAVES : 1;  // accumulator row sets
+    __shared__ uint32_t list[WAVES][CH];
+    __shared__ __attribute__((aligned(16))) float acc[ROWS][CH * NP];
+    __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
+    if (a.halt && *a.halt >= 0) return;
+    const int W = a.W, H = a.H, T = a.T;
+    // segments per tile: only the variant with neither rebuild nor fixed-order sums splits
+    const int S = (!REBUILD && !DET && a.perm_bwd) ? max(a.nseg, 1) : 1;
+    const TileGeo tg = S > 1 ? tile_geo_split(W, H, a.gx, a.gy, a.perm_bwd, a.B, S, a.nsplit)
+                             : tile_geo(W, H, a.perm_bwd, a.B);
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
+    const int lane = tg.lane, wave = tg.wave, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = 1.0f / sig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
+    const int rec_chunks = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile + 1]) & ~TN_IRREGULAR;
+    // This wave's entries: [i_begin, i_end) of the tile's recorded list.
+    int i_begin = 0, i_end = n2r;
+    if (tg.nseg > 1) {
+        i_begin = tg.seg * a.seg_m;
+        i_end = tg.seg == tg.nseg - 1 ? n2r : min(n2r, i_begin + a.seg_m);
+        if (tg.seg > 0) {
+            // the block (all of it, before any barrier) leaves when none of its
+            // four tiles has entries in this segment
+            const size_t t0 = tg.tile - (size_t)wave;
+            int most = 0;
+            for (int q = 0; q < WAVES; q++) most = max(most, (int)uniform_u32((uint32_t)a.tl_n[2 * (t0 + q)]));
+            if (most <= i_begin) return;
+        }
+    }
+
+    Back st;
+    const bool irregular = (a.tl_n[2 * tg.tile + 1] & TN_IRREGULAR) != 0;  // wave-uniform
+    {
+        int2 ze = make_int2(0, 0);
+        if (irregular) ze = a.pze[tg.tile * 64 + lane];
+        st.tot = {a.pq[tg.pix], ze.x, ze.y};
+        for (int ch = 0; ch < 3; ch++) {
+            st.g0[ch] = !tg.valid ? 0.0f
+                                  : (MODE == MODE_LOSS ? a.pg0[tg.pix * 3 + ch] : a.grad_in[img_index(a, tg.pix, b, ch)]);
+        }
+    }
+    if (i_begin > 0 && i_begin < n2r) {
+        // the forward kernel's checkpoint before entry i_begin
+        const float* c = a.ckpt + ((size_t)tg.tile * (a.nseg - 1) + (tg.seg - 1)) * (CKPT_WORDS * 64) + lane;
+        st.col[0] = c[0];
+        st.col[1] = c[64];
+        st.col[2] = c[128];
+        st.pre = {c[192], __float_as_int(c[256]), __float_as_int(c[320])};
+    } else {
+        st.col[0] = a.bg[b * 3 + 0];
+        st.col[1] = a.bg[b * 3 + 1];
+        st.col[2] = a.bg[b * 3 + 2];
+        st.pre = {1.0f, 0, 0};
+    }
+    // no lane of the tile met a zero factor or a rescaling in the forward pass
+    backward_sweep<MODE, FAST, REBUILD, DET>(a, rec, ents, tg, validm, rsig, sig, st, i_begin, i_end, rec_chunks,
+                                             !irregular, list[wave], &acc[0][0], &trans[0][0]);
     // The per-item loss (canvas.rs:45-58) from the forward kernel's per-block
     // sums, by the scene's first block, in a fixed order.
     if (MODE == MODE_LOSS && !DET && tg.bx == 0 && tg.by == 0 && tg.seg == 0 && wave == 0) {
@@ -1304,6 +1336,92 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
         l = wave_sum_f64(l);
         if (lane == 0) a.losses[b] = (float)(l / (3.0 * (double)W * (double)H));
     }
+}
+
+// The gradient paths' forward and backward in one kernel: each block
+// composites its four tiles (forward_sweep), forms dL/dpixel (MODE_LOSS: with
+// the loss partial; MODE_GRAD_IN: the caller's), then sweeps the same tiles'
+// recorded entries backward (backward_sweep) with the per-pixel state still in
+// registers, so nothing goes through HBM between the two sweeps but the entry
+// lists, and the device drains once instead of twice. Without fixed-order
+// sums and without the split backward, when every tile's list is recorded
+// whole in regions of whole 64-byte lines (cap2 >= T, cap2 % 8 == 0); both
+// sweeps take the backward kernel's block order. In MODE_LOSS sum_losses then
+// sums the scenes' loss partials.
+template <int MODE, bool FAST>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(7))) void fused_kernel(RasterArgs a, const float* __restrict__ records,
+                                                                  const TileEnt* __restrict__ ents) {
+    static_assert(MODE == MODE_LOSS || MODE == MODE_GRAD_IN, "gradient modes only");
+    __shared__ uint32_t list[WAVES][CH];
+    __shared__ double loss[WAVES];
+    __shared__ __attribute__((aligned(16))) float acc[CH * NP];
+    __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
+    if (a.halt && *a.halt >= 0) return;
+    const int W = a.W, H = a.H, T = a.T;
+    const TileGeo tg = tile_geo(W, H, a.perm_bwd, a.B);
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
+    const int lane = tg.lane, wave = tg.wave, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = 1.0f / sig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    Back st;
+    float col[3];
+    for (int ch = 0; ch < 3; ch++) col[ch] = st.col[ch] = a.bg[b * 3 + ch];
+    Trans tot = {1.0f, 0, 0};
+    int n2, rec_chunks;
+    forward_sweep<MODE, FAST, false>(a, rec, tg, validm, rsig, sig, list[wave], col, tot, n2, rec_chunks);
+    if (MODE == MODE_LOSS && a.out_img && tg.valid)
+        for (int ch = 0; ch < 3; ch++) a.out_img[img_index(a, tg.pix, b, ch)] = col[ch];
+    for (int ch = 0; ch < 3; ch++) st.g0[ch] = 0.0f;
+    double l = 0.0;
+    if (tg.valid) {
+        if (MODE == MODE_LOSS) {
+            // the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114) as forward_kernel forms them
+            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            for (int ch = 0; ch < 3; ch++) {
+                float t = a.target[img_index(a, tg.pix, b, ch)];
+                float d = col[ch] - t;
+                l += (double)d * (double)d;
+                st.g0[ch] = scale * (col[ch] - t);
+            }
+        } else {
+            for (int ch = 0; ch < 3; ch++) st.g0[ch] = a.grad_in[img_index(a, tg.pix, b, ch)];
+        }
+    }
+    if (MODE == MODE_LOSS) {
+        l = wave_sum_f64(l);
+        if (lane == 0) loss[wave] = l;
+    }
+    // The entries this wave recorded with vector stores are read back below with
+    // scalar loads: the stores are complete (in L2, which the scalar cache reads
+    // from) before any of those loads issue. A tile's region holds whole cache
+    // lines, so no scalar-cache line of it was loaded before its entries were.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (MODE == MODE_LOSS && threadIdx.x == 0) {
+        double lb = loss[0];
+        for (int q = 1; q < WAVES; q++) lb += loss[q];
+        a.partial_loss[tg.tile / WAVES] = lb;
+    }
+    st.tot = tot;
+    st.pre = {1.0f, 0, 0};
+    const bool irregular = lane_mask(tot.z != 0 || tot.e != 0) != 0;
+    backward_sweep<MODE, FAST, false, false>(a, rec, ents, tg, validm, rsig, sig, st, 0, n2, rec_chunks, !irregular,
+                                             list[wave], acc, &trans[0][0]);
+}
+
+// The per-item loss (canvas.rs:45-58) from the fused kernel's per-block sums,
+// one wave per scene, in the order of backward_kernel's sum.
+__global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ partial_loss, int nblk, double npix3,
+                                                 float* __restrict__ losses, const int* __restrict__ halt) {
+    if (halt && *halt >= 0) return;
+    const int b = (int)blockIdx.x, lane = (int)threadIdx.x;
+    const double* pl = partial_loss + (size_t)b * nblk;
+    double l = 0.0;
+    for (int r = lane; r < nblk; r += 64) l += pl[r];
+    l = wave_sum_f64(l);
+    if (lane == 0) losses[b] = (float)(l / npix3);
 }
 
 // Sum the per-block partial rows of each scene in block order. One block per
@@ -1571,6 +1689,34 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
                     : launch_backward_r<MODE_LOSS, false>(rebuild, a, s);
     return fast ? launch_backward_r<MODE_GRAD_IN, true>(rebuild, a, s)
                 : launch_backward_r<MODE_GRAD_IN, false>(rebuild, a, s);
+}
+
+template <int MODE>
+static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
+    if (fast)
+        hipLaunchKernelGGL((fused_kernel<MODE, true>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+    else
+        hipLaunchKernelGGL((fused_kernel<MODE, false>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+}
+
+hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
+    if ((size_t)a.B * a.H * a.W == 0) return hipSuccess;
+    if ((mode != MODE_LOSS && mode != MODE_GRAD_IN) || a.cap2 < a.T || a.cap2 % 8 != 0 || a.deterministic ||
+        a.nseg > 1)
+        return hipErrorInvalidValue;
+    const dim3 grid = raster_grid(a.B, a.W, a.H);
+    if (mode == MODE_LOSS)
+        launch_fused_m<MODE_LOSS>(fast, a, grid, s);
+    else
+        launch_fused_m<MODE_GRAD_IN>(fast, a, grid, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, double npix3, float* losses, hipStream_t s,
+                             const int* halt) {
+    if (B == 0) return hipSuccess;
+    hipLaunchKernelGGL(sum_losses, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+    return hipGetLastError();
 }
 
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,

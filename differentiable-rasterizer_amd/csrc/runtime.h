@@ -237,6 +237,7 @@ struct RasterBufs {
     int cap2 = 0;
     float* ckpt = nullptr;          // split backward's checkpoints, or null: no split
     int nseg = 1, seg_m = 0, nsplit = 0;  // its segments, entries per segment, split blocks per scene
+    bool fused = false;             // one fused kernel (fused_gradients); pq, pg0, pze, tn unused
 };
 
 // Split of the backward's sweep over a tile's recorded entries. A tile's sweep
@@ -260,6 +261,14 @@ int backward_segments(int T, int cap2, bool det, size_t blocks, int cus);
 // and (gradient modes) the backward pass and the partial-row reduction. With
 // `halt`, every kernel does nothing once *halt >= 0.
 // `timed`: the launches take part in drh_timing_* (events are created for them).
+// Whether a gradient-mode call runs as one fused kernel (forward and backward
+// sweeps of each block together, both in the backward's block order): when
+// every list is recorded whole in line-aligned regions (cap2 >= T, cap2 % 8 ==
+// 0), without fixed-order sums and without the split backward (which a grid
+// too small to fill the device takes instead). DRH_UNFUSED=1 in the
+// environment keeps the two kernels (for comparing the two paths).
+bool fused_gradients(int mode, bool det, int nseg, int cap2, int T);
+
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
                     uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt = nullptr,

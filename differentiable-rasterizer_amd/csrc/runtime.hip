@@ -289,6 +289,13 @@ bool use_order(const drh_ctx* ctx, int B, int gx, int gy) {
            (size_t)(gx + 1) * (gy + 1) <= (size_t)drh::ORD_MAX_CELLS;
 }
 
+bool fused_gradients(int mode, bool det, int nseg, int cap2, int T) {
+    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || det || nseg > 1 || cap2 < T || cap2 % 8 != 0)
+        return false;
+    const char* e = std::getenv("DRH_UNFUSED");
+    return !(e && e[0] == '1');
+}
+
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
                     uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt, bool timed) {
@@ -338,6 +345,17 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.gx = (int)grid.x;
     a.gy = (int)grid.y;
     a.ckpt = bufs.ckpt;
+    if (bufs.fused) {
+        {
+            KernelTimer kt(ctx, TK_RASTER, s, timed);
+            HIP_TRY(drh::launch_fused(mode, fast, a, s), "fused_kernel launch");
+        }
+        if (mode != drh::MODE_LOSS) return DRH_OK;
+        KernelTimer kt(ctx, TK_REDUCE, s, timed);
+        HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, 3.0 * (double)H * (double)W, out_losses, s, halt),
+                "sum_losses launch");
+        return DRH_OK;
+    }
     {
         KernelTimer kt(ctx, TK_RASTER, s, timed);
         HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
@@ -369,20 +387,10 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     const size_t ntiles = (size_t)B * nblk * drh::WAVES;
     Lease rec, partials, ploss, pq, pg0, pze, tent, tn, order, ckpt;
     RasterBufs bufs;
-    bufs.cap2 = tile_entries(ntiles, T);
+    // whole 64-byte lines per tile (8 entries), as the fused kernel needs
+    bufs.cap2 = tile_entries(ntiles, (T + 7) & ~7);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
-    if (mode != drh::MODE_RENDER) {
-        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
-            return rc;
-        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
-        if ((rc = pq.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(float), s))) return rc;
-        if (mode == drh::MODE_LOSS && (rc = pg0.acquire(ctx, K_PIX_G0, (size_t)B * H * W * 3 * sizeof(float), s)))
-            return rc;
-        if ((rc = pze.acquire(ctx, K_PIX_ZE, ntiles * 64 * sizeof(int2), s))) return rc;
-        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
-        if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
-    }
     if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
         if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
         bufs.order = order.get<int>();
@@ -394,6 +402,22 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
             bufs.nseg = nseg;
             bufs.seg_m = (T + SPLIT_DIVISOR - 1) / SPLIT_DIVISOR;
             bufs.nsplit = std::max(1, nblk / SPLIT_BLOCK_SHARE);
+        }
+    }
+    bufs.fused = fused_gradients(mode, det, bufs.nseg, bufs.cap2, T);
+    if (mode != drh::MODE_RENDER) {
+        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
+            return rc;
+        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
+        if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
+        // the hand-over between the two kernels (the fused kernel keeps it in registers)
+        if (!bufs.fused) {
+            if ((rc = pq.acquire(ctx, K_PIXSTATE, (size_t)B * H * W * sizeof(float), s))) return rc;
+            if (mode == drh::MODE_LOSS &&
+                (rc = pg0.acquire(ctx, K_PIX_G0, (size_t)B * H * W * 3 * sizeof(float), s)))
+                return rc;
+            if ((rc = pze.acquire(ctx, K_PIX_ZE, ntiles * 64 * sizeof(int2), s))) return rc;
+            if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
         }
     }
     bufs.rec = rec.get<float>();

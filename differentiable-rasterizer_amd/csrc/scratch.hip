@@ -71,7 +71,7 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     if (det) off = up(off + (size_t)B * nblk * T * NP * sizeof(float));
     L.tent = off;
     const size_t left = SCRATCH_BYTES > off ? SCRATCH_BYTES - off : 0;
-    L.cap2 = tile_entries(ntiles, T, left, 1);
+    L.cap2 = tile_entries(ntiles, (T + 7) & ~7, left, 1);  // whole 64-byte lines per tile, as the fused kernel needs
     L.total = up(off + ntiles * (size_t)L.cap2 * sizeof(drh::TileEnt));
     return L;
 }
@@ -128,6 +128,7 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
     bufs.partials = det ? reinterpret_cast<float*>(base + L.partials) : nullptr;
     bufs.tent = reinterpret_cast<drh::TileEnt*>(base + L.tent);
     bufs.cap2 = L.cap2;
+    bufs.fused = fused_gradients(drh::MODE_LOSS, det, bufs.nseg, bufs.cap2, (int)T);
     // Nothing in the scratch array needs to start at zero: every buffer is
     // written by this call's kernels before it is read (the gradients are the
     // caller's output and setup_records clears them).

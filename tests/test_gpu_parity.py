@@ -83,6 +83,31 @@ def test_backward_from_grad_matches_oracle(ctx, orc, name, B, H, W, T, sigma, ki
     assert_grads(gpu, inv, label=f"{name} inverted")
 
 
+@pytest.mark.parametrize("name,B,H,W,T,sigma,kind", [CASES[0], CASES[1], CASES[4]],
+                         ids=[CASES[0][0], CASES[1][0], CASES[4][0]])
+def test_fused_and_two_kernel_paths_agree(ctx, orc, name, B, H, W, T, sigma, kind, monkeypatch):
+    # The gradient paths run as one fused kernel; DRH_UNFUSED=1 keeps
+    # forward_kernel and backward_kernel, the path that fixed-order sums, the
+    # split backward and the rebuild past the recorded entries take. The loss
+    # and image come from the same per-block sums (bit-equal); the gradients
+    # differ only in the order of their float atomics.
+    params, bgs = make_case(B, H, W, T, kind)
+    targets = orc.render_batch(synth.batch(kind, B, T, 100, target_offset=1000), H, W, sigma, bgs[::-1].copy())
+    gin = ((synth.uniforms(8, B * H * W * 3) - 0.5) * 1e-3).reshape(B, H, W, 3).astype(np.float32)
+    print(f"fused vs two kernels {name}", flush=True)
+    fl, fg, fimg = ctx.fused_loss_backward(params, targets, sigma, bgs, want_images=True)
+    ff = ctx.backward_from_grad(params, gin, sigma, bgs)
+    monkeypatch.setenv("DRH_UNFUSED", "1")
+    ul, ug, uimg = ctx.fused_loss_backward(params, targets, sigma, bgs, want_images=True)
+    uf = ctx.backward_from_grad(params, gin, sigma, bgs)
+    assert np.array_equal(fl, ul) and np.array_equal(fimg, uimg)
+    assert grad_err(fg, ug) <= 1e-6 and grad_err(ff, uf) <= 1e-6
+    cl, cg = orc.loss_backward_batch(params, targets, sigma, bgs)
+    check_losses(ul, cl)
+    assert_grads(ug, cg, label=f"two kernels {name}")
+    assert_grads(uf, orc.backward_from_grad_batch(params, gin, sigma, bgs), label=f"two kernels from_grad {name}")
+
+
 @pytest.mark.parametrize("mode", ["loss", "from_grad"])
 def test_split_backward_matches_oracle(ctx, orc, mode):
     # Six 128x128 scenes of large triangles: 384 blocks, under six per compute
