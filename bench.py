@@ -1,19 +1,20 @@
 #!/usr/bin/env python3
 """Benchmark: batched soft-raster forward + MSE + backward on one MI355X.
 
-One step = one drh_fused_loss_backward call (setup_records, forward_kernel,
-backward_kernel) over the headline workload: B=16 scenes at 256x256,
+One step = one drh_fused_loss_backward call (setup_records, fused_kernel,
+sum_losses) over the headline workload: B=16 scenes at 256x256,
 T=128 triangles each, sigma=0.0015, synthetic seeded scenes (diffrast.synth)
 and targets rendered from independently seeded scenes. Inputs and outputs
 stay in HBM; the timed region is K steps between two synchronizations.
 
 Printed (one JSON line on stdout): throughput in dense pixel-triangle
 evaluations per second, ms per batch, the dominant kernel's roofline position
-(backward_kernel: its algorithmic FLOP per launch over its event-timed average
-duration, against the FP32 vector peak; the forward kernel and the pair are
-reported beside it), the CPU baseline (the C oracle, one thread per scene, on
-this host's cores), and under "configs" the same measurements for every
-benchmark workload: c0 (B=1 64x64 T=32), c1 (B=16 128x128 T=128), c2 (the
+(fused_kernel: its algorithmic FLOP per launch over its event-timed average
+duration, against the FP32 vector peak; under "two_kernel_path" the same step
+with forward_kernel and backward_kernel, DRH_UNFUSED=1, and their rooflines;
+configurations that take the two kernels report them directly), the CPU
+baseline (the C oracle, one thread per scene, on this host's cores), and under
+"configs" the same measurements for every benchmark workload: c0 (B=1 64x64 T=32), c1 (B=16 128x128 T=128), c2 (the
 headline), c3 (B=8 256x256 T=512 small triangles) and c4 (the 800-iteration
 fit at 176x176, T=150, against the oracle's fit on one core).
 
@@ -106,16 +107,23 @@ def time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev):
     return ms, losses, grads
 
 
-def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev):
-    """Event-timed average duration of each kernel of the step."""
+def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev, two_kernels=False):
+    """Event-timed average duration of each kernel of the step: setup_records, then
+    either fused_kernel and sum_losses, or (two_kernels: DRH_UNFUSED=1, and the
+    paths that always take them) forward_kernel and backward_kernel."""
+    if two_kernels:
+        os.environ["DRH_UNFUSED"] = "1"
     ctx.timing(True)
     try:
         time_fused(torch, ctx, cfg, p, bg, targets, steps, 0, dev)
         t = ctx.read_timings()
     finally:
         ctx.timing(False)
-    names = {"setup": "setup", "forward": "raster", "backward": "backward", "reduce": "reduce"}
-    return {k: t[f"{f}_ms"] / max(t[f"{f}_n"], 1) for k, f in names.items()}
+        os.environ.pop("DRH_UNFUSED", None)
+    ms = {f: t[f"{f}_ms"] / max(t[f"{f}_n"], 1) for f in ("setup", "raster", "backward", "reduce")}
+    if t["backward_n"] == 0 and t["raster_n"] > 0:
+        return {"setup": ms["setup"], "fused": ms["raster"], "sum_losses": ms["reduce"]}
+    return {"setup": ms["setup"], "forward": ms["raster"], "backward": ms["backward"], "reduce": ms["reduce"]}
 
 
 def traffic_from_profiles(kernel):
@@ -341,6 +349,17 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
     ms, losses, grads = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)
     kt = kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(steps, 50)), dev)
     log(f"{name}: {ms:.4f} ms/batch over {steps} steps; kernel avg ms {kt}")
+    # the same step on the two-kernel path, for its per-kernel figures
+    two = None
+    if "fused" in kt:
+        os.environ["DRH_UNFUSED"] = "1"
+        try:
+            ms2 = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)[0]
+        finally:
+            os.environ.pop("DRH_UNFUSED", None)
+        two = {"ms_per_batch": ms2,
+               "kernel_ms": kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(steps, 50)), dev, True)}
+        log(f"{name}: two-kernel path {ms2:.4f} ms/batch; kernel avg ms {two['kernel_ms']}")
     dense = B * H * W * T
     out = {
         "workload": f"batched soft-raster forward+MSE+backward, B={B} {H}x{W} T={T} sigma={SIGMA}"
@@ -368,13 +387,26 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
     counts = (c["n_box"], c["n_contrib"], B * H * W)
     flop_f = sum(a * b for a, b in zip(FLOP_FWD, counts))
     flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
-    out["roofline"] = roof("backward_kernel", flop_b, kt["backward"],
-                           traffic_from_profiles("backward_kernel") if traffic else None)
+    def two_kernel_roofs(k):
+        return {"roofline_backward": roof("backward_kernel", flop_b, k["backward"],
+                                          traffic_from_profiles("backward_kernel") if traffic else None),
+                "roofline_forward": roof("forward_kernel", flop_f, k["forward"],
+                                         traffic_from_profiles("forward_kernel") if traffic else None),
+                "roofline_pair": roof("forward_kernel+backward_kernel", flop_f + flop_b,
+                                      k["forward"] + k["backward"])}
+
+    if "fused" in kt:
+        out["roofline"] = roof("fused_kernel", flop_f + flop_b, kt["fused"],
+                               traffic_from_profiles("fused_kernel") if traffic else None)
+        two.update(two_kernel_roofs(two["kernel_ms"]))
+        two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
+        out["two_kernel_path"] = two
+    else:
+        r = two_kernel_roofs(kt)
+        out["roofline"] = r.pop("roofline_backward")
+        out.update(r)
     out["roofline"]["n_box_pairs"] = c["n_box"]
     out["roofline"]["n_contrib_pairs"] = c["n_contrib"]
-    out["roofline_forward"] = roof("forward_kernel", flop_f, kt["forward"],
-                                   traffic_from_profiles("forward_kernel") if traffic else None)
-    out["roofline_pair"] = roof("forward_kernel+backward_kernel", flop_f + flop_b, kt["forward"] + kt["backward"])
     out["roofline_step"] = roof("whole step (wall)", flop_f + flop_b, ms)
     out["cpu_baseline"] = {
         "value": dense / c["per_batch_s"],
@@ -491,9 +523,8 @@ def main():
         "kernel_ms": head["kernel_ms"],
         "parity_vs_oracle": head.get("parity_vs_oracle"),
         "roofline": head.get("roofline"),
-        "roofline_forward": head.get("roofline_forward"),
-        "roofline_pair": head.get("roofline_pair"),
         "roofline_step": head.get("roofline_step"),
+        "two_kernel_path": head.get("two_kernel_path"),
         "cpu_baseline": head.get("cpu_baseline"),
     }
     if not args.no_side:

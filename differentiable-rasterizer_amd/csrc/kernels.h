@@ -166,8 +166,9 @@ hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& a, hipStream_t s);
 // Forward and backward of a gradient mode in one kernel (hipErrorInvalidValue
-// unless cap2 >= T, cap2 % 8 == 0, not deterministic, no split); in MODE_LOSS
-// launch_sum_losses then forms the per-scene losses from its per-block partials.
+// unless cap2 >= T, cap2 % 8 == 0 and no split); then launch_reduce
+// (deterministic) or, in MODE_LOSS, launch_sum_losses forms the results from
+// its per-block sums.
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, double npix3, float* losses, hipStream_t s,
                              const int* halt = nullptr);

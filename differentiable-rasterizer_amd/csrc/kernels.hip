@@ -67,8 +67,8 @@ struct BlockBox {
     int x0, y0, x1, y1;
 };
 
-// The box of triangle p as setup_one makes it (raster.rs:26-28, 144-168), for
-// the block-order estimate of another workgroup than the one that sets it up.
+// The cull box of triangle p (raster.rs:26-28, 144-168) in 16x16 blocks, for
+// the block-order estimate (a taped forward's liveness: alpha > 0).
 __device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, float sigma) {
     float v[6];
     bool finite = true;
@@ -87,10 +87,9 @@ __device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, 
     return bb;
 }
 
-// Setup of triangle i (scene-major index): its record, and its box in blocks
-// (empty when the triangle is not drawn).
-__device__ inline BlockBox setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
-                                     int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
+// Setup of triangle i (scene-major index): its record.
+__device__ inline void setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
+                                 int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
     // The backward kernel adds into the gradients: they start at zero.
     if (zero_grads)
         for (int j = 0; j < NP; j++) zero_grads[i * NP + j] = 0.0f;
@@ -205,9 +204,6 @@ __device__ inline BlockBox setup_one(const float* __restrict__ params, size_t i,
         eb[6] = 0.0f;
         eb[7] = 0.0f;
     }
-    BlockBox bb = {1, 1, 0, 0};
-    if (live) bb = {bx0 >> 4, by0 >> 4, (bx1 - 1) >> 4, (by1 - 1) >> 4};
-    return bb;
 }
 
 // The raster kernels' block order, heaviest first. A block's time follows its
@@ -269,10 +265,11 @@ __device__ inline void order_scene(const OrderArgs& o, int* cells, int b, int T)
     for (int blk = t; blk < nb; blk += SETUP_THREADS) o.perm[(size_t)b * nb + atomicAdd(&hist[key(blk)], 1)] = blk;
 }
 
-// Workgroup (x, b): the records of scene b's triangles [x n, x n + n), n the
-// workgroup size, and, for x == 0 with o.perm (then n == SETUP_THREADS), the
-// scene's block order from all its boxes (those of the other workgroups'
-// triangles are computed again here, which is cheap).
+// Workgroup (x, b) with x < nrec = ceil(T / n), n the workgroup size: the
+// records of scene b's triangles [x n, x n + n). With o.perm (then
+// n == SETUP_THREADS), workgroup (nrec, b) makes the scene's block order from
+// the triangles' boxes, computed again from the parameters, concurrently with
+// the records.
 __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __restrict__ params, int T, int W,
                                                                int H, float sigma, int setup_mode,
                                                                float* __restrict__ rec, float* __restrict__ zero_grads,
@@ -282,20 +279,20 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
                                                                RecordHead* __restrict__ head, RecordHead head_val) {
     __shared__ int cells[ORD_MAX_CELLS];
     if (halt && *halt >= 0) return;
-    const int b = blockIdx.y, k = blockIdx.x * blockDim.x + threadIdx.x, pitch = o.gx + 1;
+    const int b = blockIdx.y, pitch = o.gx + 1;
+    const int nrec = (T + (int)blockDim.x - 1) / (int)blockDim.x;
     if (head && b == 0 && blockIdx.x == 0 && threadIdx.x == 0) *head = head_val;
-    const bool order = o.perm && blockIdx.x == 0;
     // A record kept for a later backward holds its own copy of the backgrounds.
     if (bg_dst && blockIdx.x == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
-    if (order) {
-        for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
-        __syncthreads();
+    if (!o.perm || (int)blockIdx.x < nrec) {
+        const int k = blockIdx.x * blockDim.x + threadIdx.x;
+        if (k < T) setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
+        return;
     }
-    BlockBox bb = {1, 1, 0, 0};
-    if (k < T) bb = setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
-    if (!order) return;
+    for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
+    __syncthreads();
     for (int q = threadIdx.x; q < T; q += SETUP_THREADS) {
-        if (q >= SETUP_THREADS) bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma);
+        const BlockBox bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma);
         if (bb.x0 <= bb.x1 && bb.y0 <= bb.y1) {
             atomicAdd(&cells[bb.y0 * pitch + bb.x0], 1);
             atomicAdd(&cells[bb.y0 * pitch + bb.x1 + 1], -1);
@@ -1343,18 +1340,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
 // the loss partial; MODE_GRAD_IN: the caller's), then sweeps the same tiles'
 // recorded entries backward (backward_sweep) with the per-pixel state still in
 // registers, so nothing goes through HBM between the two sweeps but the entry
-// lists, and the device drains once instead of twice. Without fixed-order
-// sums and without the split backward, when every tile's list is recorded
-// whole in regions of whole 64-byte lines (cap2 >= T, cap2 % 8 == 0); both
-// sweeps take the backward kernel's block order. In MODE_LOSS sum_losses then
-// sums the scenes' loss partials.
-template <int MODE, bool FAST>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(7))) void fused_kernel(RasterArgs a, const float* __restrict__ records,
-                                                                  const TileEnt* __restrict__ ents) {
+// lists, and the device drains once instead of twice. Without the split
+// backward, when every tile's list is recorded whole in regions of whole
+// 64-byte lines (cap2 >= T, cap2 % 8 == 0); both sweeps take the backward
+// kernel's block order. Then reduce_partials (DET) or, in MODE_LOSS,
+// sum_losses forms the results from the per-block sums.
+// DET: per-wave accumulator rows and partial rows per block, as backward_kernel.
+template <int MODE, bool FAST, bool DET>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET ? 4 : 7))) void fused_kernel(RasterArgs a, const float* __restrict__ records,
+                                                                            const TileEnt* __restrict__ ents) {
     static_assert(MODE == MODE_LOSS || MODE == MODE_GRAD_IN, "gradient modes only");
+    constexpr int ROWS = DET ? WAVES : 1;  // accumulator row sets
     __shared__ uint32_t list[WAVES][CH];
     __shared__ double loss[WAVES];
-    __shared__ __attribute__((aligned(16))) float acc[CH * NP];
+    __shared__ __attribute__((aligned(16))) float acc[ROWS * CH * NP];
     __shared__ __attribute__((aligned(16))) float trans[WAVES][NP * TP];
     if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
@@ -1407,8 +1406,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(7)))
     st.tot = tot;
     st.pre = {1.0f, 0, 0};
     const bool irregular = lane_mask(tot.z != 0 || tot.e != 0) != 0;
-    backward_sweep<MODE, FAST, false, false>(a, rec, ents, tg, validm, rsig, sig, st, 0, n2, rec_chunks, !irregular,
-                                             list[wave], acc, &trans[0][0]);
+    backward_sweep<MODE, FAST, false, DET>(a, rec, ents, tg, validm, rsig, sig, st, 0, n2, rec_chunks, !irregular,
+                                           list[wave], acc, &trans[0][0]);
 }
 
 // The per-item loss (canvas.rs:45-58) from the fused kernel's per-block sums,
@@ -1623,9 +1622,10 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
                         const OrderArgs& o, const int* halt, RecordHead* head, const RecordHead& head_val) {
     if (B == 0 || (T == 0 && !bg_dst && !o.perm && !head)) return hipSuccess;
     if (o.perm && (o.gy + 1) * (o.gx + 1) > ORD_MAX_CELLS) return hipErrorInvalidValue;
-    // without an order, small workgroups spread the triangles over more CUs
+    // without an order, small workgroups spread the triangles over more CUs;
+    // with one, a last workgroup per scene makes it
     const int n = o.perm ? SETUP_THREADS : 64;
-    const int gx = T > 0 ? (T + n - 1) / n : 1;
+    const int gx = (T + n - 1) / n + (o.perm || T == 0 ? 1 : 0);
     hipLaunchKernelGGL(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
                        zero_grads, bg_src, bg_dst, o, halt, head, head_val);
     return hipGetLastError();
@@ -1691,18 +1691,25 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
                 : launch_backward_r<MODE_GRAD_IN, false>(rebuild, a, s);
 }
 
+template <int MODE, bool DET>
+static void launch_fused_d(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
+    if (fast)
+        hipLaunchKernelGGL((fused_kernel<MODE, true, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+    else
+        hipLaunchKernelGGL((fused_kernel<MODE, false, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+}
+
 template <int MODE>
 static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
-    if (fast)
-        hipLaunchKernelGGL((fused_kernel<MODE, true>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+    if (a.deterministic)
+        launch_fused_d<MODE, true>(fast, a, grid, s);
     else
-        hipLaunchKernelGGL((fused_kernel<MODE, false>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+        launch_fused_d<MODE, false>(fast, a, grid, s);
 }
 
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
     if ((size_t)a.B * a.H * a.W == 0) return hipSuccess;
-    if ((mode != MODE_LOSS && mode != MODE_GRAD_IN) || a.cap2 < a.T || a.cap2 % 8 != 0 || a.deterministic ||
-        a.nseg > 1)
+    if ((mode != MODE_LOSS && mode != MODE_GRAD_IN) || a.cap2 < a.T || a.cap2 % 8 != 0 || a.nseg > 1)
         return hipErrorInvalidValue;
     const dim3 grid = raster_grid(a.B, a.W, a.H);
     if (mode == MODE_LOSS)

@@ -264,10 +264,10 @@ int backward_segments(int T, int cap2, bool det, size_t blocks, int cus);
 // Whether a gradient-mode call runs as one fused kernel (forward and backward
 // sweeps of each block together, both in the backward's block order): when
 // every list is recorded whole in line-aligned regions (cap2 >= T, cap2 % 8 ==
-// 0), without fixed-order sums and without the split backward (which a grid
-// too small to fill the device takes instead). DRH_UNFUSED=1 in the
-// environment keeps the two kernels (for comparing the two paths).
-bool fused_gradients(int mode, bool det, int nseg, int cap2, int T);
+// 0) and without the split backward (which a grid too small to fill the
+// device takes instead). DRH_UNFUSED=1 in the environment keeps the two
+// kernels (for comparing the two paths).
+bool fused_gradients(int mode, int nseg, int cap2, int T);
 
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,

@@ -289,8 +289,8 @@ bool use_order(const drh_ctx* ctx, int B, int gx, int gy) {
            (size_t)(gx + 1) * (gy + 1) <= (size_t)drh::ORD_MAX_CELLS;
 }
 
-bool fused_gradients(int mode, bool det, int nseg, int cap2, int T) {
-    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || det || nseg > 1 || cap2 < T || cap2 % 8 != 0)
+bool fused_gradients(int mode, int nseg, int cap2, int T) {
+    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || nseg > 1 || cap2 < T || cap2 % 8 != 0)
         return false;
     const char* e = std::getenv("DRH_UNFUSED");
     return !(e && e[0] == '1');
@@ -346,30 +346,27 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.gy = (int)grid.y;
     a.ckpt = bufs.ckpt;
     if (bufs.fused) {
+        KernelTimer kt(ctx, TK_RASTER, s, timed);
+        HIP_TRY(drh::launch_fused(mode, fast, a, s), "fused_kernel launch");
+    } else {
         {
             KernelTimer kt(ctx, TK_RASTER, s, timed);
-            HIP_TRY(drh::launch_fused(mode, fast, a, s), "fused_kernel launch");
+            HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
         }
-        if (mode != drh::MODE_LOSS) return DRH_OK;
-        KernelTimer kt(ctx, TK_REDUCE, s, timed);
-        HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, 3.0 * (double)H * (double)W, out_losses, s, halt),
-                "sum_losses launch");
-        return DRH_OK;
-    }
-    {
-        KernelTimer kt(ctx, TK_RASTER, s, timed);
-        HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
-    }
-    if (mode == drh::MODE_RENDER) return DRH_OK;
-    {
+        if (mode == drh::MODE_RENDER) return DRH_OK;
         KernelTimer kt(ctx, TK_BACKWARD, s, timed);
         HIP_TRY(drh::launch_backward(mode, fast, bufs.cap2 < T, a, s), "backward_kernel launch");
     }
-    if (!det) return DRH_OK;
-    KernelTimer kt(ctx, TK_REDUCE, s, timed);
-    HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3.0 * (double)H * (double)W, out_grads,
-                               mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
-            "reduce_partials launch");
+    if (det) {
+        KernelTimer kt(ctx, TK_REDUCE, s, timed);
+        HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3.0 * (double)H * (double)W, out_grads,
+                                   mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
+                "reduce_partials launch");
+    } else if (bufs.fused && mode == drh::MODE_LOSS) {
+        KernelTimer kt(ctx, TK_REDUCE, s, timed);
+        HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, 3.0 * (double)H * (double)W, out_losses, s, halt),
+                "sum_losses launch");
+    }
     return DRH_OK;
 }
 
@@ -404,7 +401,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
             bufs.nsplit = std::max(1, nblk / SPLIT_BLOCK_SHARE);
         }
     }
-    bufs.fused = fused_gradients(mode, det, bufs.nseg, bufs.cap2, T);
+    bufs.fused = fused_gradients(mode, bufs.nseg, bufs.cap2, T);
     if (mode != drh::MODE_RENDER) {
         if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
             return rc;

@@ -128,7 +128,7 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
     bufs.partials = det ? reinterpret_cast<float*>(base + L.partials) : nullptr;
     bufs.tent = reinterpret_cast<drh::TileEnt*>(base + L.tent);
     bufs.cap2 = L.cap2;
-    bufs.fused = fused_gradients(drh::MODE_LOSS, det, bufs.nseg, bufs.cap2, (int)T);
+    bufs.fused = fused_gradients(drh::MODE_LOSS, bufs.nseg, bufs.cap2, (int)T);
     // Nothing in the scratch array needs to start at zero: every buffer is
     // written by this call's kernels before it is read (the gradients are the
     // caller's output and setup_records clears them).

@@ -90,18 +90,26 @@ def test_fused_and_two_kernel_paths_agree(ctx, orc, name, B, H, W, T, sigma, kin
     # forward_kernel and backward_kernel, the path that fixed-order sums, the
     # split backward and the rebuild past the recorded entries take. The loss
     # and image come from the same per-block sums (bit-equal); the gradients
-    # differ only in the order of their float atomics.
+    # differ only in the order of their float atomics, and not at all with
+    # fixed-order sums.
     params, bgs = make_case(B, H, W, T, kind)
     targets = orc.render_batch(synth.batch(kind, B, T, 100, target_offset=1000), H, W, sigma, bgs[::-1].copy())
     gin = ((synth.uniforms(8, B * H * W * 3) - 0.5) * 1e-3).reshape(B, H, W, 3).astype(np.float32)
     print(f"fused vs two kernels {name}", flush=True)
-    fl, fg, fimg = ctx.fused_loss_backward(params, targets, sigma, bgs, want_images=True)
-    ff = ctx.backward_from_grad(params, gin, sigma, bgs)
+
+    def run():
+        return (ctx.fused_loss_backward(params, targets, sigma, bgs, want_images=True),
+                ctx.backward_from_grad(params, gin, sigma, bgs),
+                ctx.fused_loss_backward(params, targets, sigma, bgs, deterministic=True),
+                ctx.backward_from_grad(params, gin, sigma, bgs, deterministic=True))
+
+    (fl, fg, fimg), ff, (fdl, fdg), fdf = run()
     monkeypatch.setenv("DRH_UNFUSED", "1")
-    ul, ug, uimg = ctx.fused_loss_backward(params, targets, sigma, bgs, want_images=True)
-    uf = ctx.backward_from_grad(params, gin, sigma, bgs)
+    (ul, ug, uimg), uf, (udl, udg), udf = run()
     assert np.array_equal(fl, ul) and np.array_equal(fimg, uimg)
     assert grad_err(fg, ug) <= 1e-6 and grad_err(ff, uf) <= 1e-6
+    assert np.array_equal(fdl, udl) and np.array_equal(fdg, udg) and np.array_equal(fdf, udf)
+    assert np.array_equal(fdl, fl)
     cl, cg = orc.loss_backward_batch(params, targets, sigma, bgs)
     check_losses(ul, cl)
     assert_grads(ug, cg, label=f"two kernels {name}")
