@@ -212,13 +212,13 @@ def fit_config(ctx, with_cpu=True):
     return out
 
 
-def torch_op_ms(torch, cfg, p, targets, dev, steps=10):
+def torch_op_ms(torch, cfg, p, targets, dev, steps=50):
     """End to end through the drop-in autograd op: fused_mse forward + backward."""
     from diffrast import torch_layer
 
     tgt = targets.permute(0, 3, 1, 2).contiguous()
     q = p.clone().requires_grad_(True)
-    for _ in range(3):
+    for _ in range(10):
         torch_layer.fused_mse(q, tgt, sigma=SIGMA).backward()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -229,7 +229,7 @@ def torch_op_ms(torch, cfg, p, targets, dev, steps=10):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=10):
+def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=50):
     """End to end through the drop-in autograd op: rasterize, an MSE in torch, backward.
     keep_record=False times the backward that renders again, as the reference's does."""
     from diffrast import torch_layer
@@ -242,7 +242,7 @@ def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=10):
                                            keep_record)
         ((img - tgt) ** 2).mean().backward()
 
-    for _ in range(3):
+    for _ in range(10):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
