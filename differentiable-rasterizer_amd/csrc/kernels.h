@@ -170,8 +170,12 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
 // (deterministic) or, in MODE_LOSS, launch_sum_losses forms the results from
 // its per-block sums.
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s);
-hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, double npix3, float* losses, hipStream_t s,
-                             const int* halt = nullptr);
+// per: loss partials per block (1, or WAVES for the fused kernel's per-tile partials outside the
+// deterministic mode).
+hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int per, double npix3, float* losses,
+                             hipStream_t s, const int* halt = nullptr);
+// Loss partials per block that a gradient call's raster kernels write.
+constexpr int loss_partials_per_block(bool fused, bool deterministic) { return fused && !deterministic ? WAVES : 1; }
 // npix3: 3 H W, the divisor of the per-item loss (canvas.rs:45-58)
 hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
                          double npix3, float* grads, float* losses, hipStream_t s, const int* halt = nullptr);

@@ -784,11 +784,13 @@ struct TileGeo {
 };
 
 // The tile of this wave in block (bx, by) of scene b, gx x gy blocks per scene.
+// wave: the tile of the block (-1: this wave's place in a block of WAVES waves).
 __device__ inline TileGeo tile_at(int W, int H, int gx, int gy, int b, int bx, int by, int rank, int seg,
-                                  int nseg) {
+                                  int nseg, int wave = -1) {
     TileGeo t;
     t.lane = threadIdx.x & 63;
-    t.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar tile indices
+    // uniform: scalar tile indices
+    t.wave = wave >= 0 ? wave : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     t.b = b;
     t.rank = rank;
     t.seg = seg;
@@ -832,6 +834,25 @@ __device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int 
         by = local / gx;
     }
     return tile_at(W, H, gx, gy, b, bx, by, rank, 0, 1);
+}
+
+// One wave per workgroup, B nb WAVES slots in one dimension: slot i is tile
+// i % WAVES of the block at rank i / (WAVES B) of scene (i / WAVES) % B, so the
+// four tiles of each block by setup_records' order (perm, heaviest first) run
+// in consecutive slots; without perm, block order.
+__device__ inline TileGeo tile_geo_wave(int W, int H, int gx, int gy, const int* perm, int B) {
+    const int nb = gx * gy, i = (int)blockIdx.x, wave = i % WAVES;
+    int b, rank, local;
+    if (perm) {
+        b = (i / WAVES) % B;
+        rank = i / (WAVES * B);
+        local = min(max(perm[(size_t)b * nb + rank], 0), nb - 1);
+    } else {
+        b = i / (WAVES * nb);
+        rank = -1;
+        local = (i / WAVES) % nb;
+    }
+    return tile_at(W, H, gx, gy, b, local % gx, local / gx, rank, 0, 1, wave);
 }
 
 // The split backward's grid: B (nb + K (S - 1)) slots in one dimension. The
@@ -1246,6 +1267,28 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
     }
 }
 
+// reduce_entry's wave sum, added by lane 4p straight into parameter p of the
+// triangle's gradient row `grow` in global memory (one float atomic each).
+__device__ inline void reduce_entry_global(const float (&a)[NP], lds_float* tw, float* grow, int lane) {
+    for (int q = 0; q < NP; q++) tw[q * TP + lane] = a[q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int prm = min(lane >> 2, NP - 1), g = lane & 3;
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) f4v lds_f4v;
+    const lds_f4v* src = reinterpret_cast<const lds_f4v*>(tw + prm * TP + 16 * g);
+    const f4v x0 = src[0], x1 = src[1], x2 = src[2], x3 = src[3];
+    float sum = (((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w))) +
+                (((x2.x + x2.y) + (x2.z + x2.w)) + ((x3.x + x3.y) + (x3.z + x3.w)));
+    sum += dpp<DPP_XOR1>(sum);
+    sum += dpp<DPP_XOR2>(sum);
+    if (g == 0 && lane < 4 * NP && sum != 0.0f) unsafeAtomicAdd(grow + prm, sum);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
 // forward kernel recorded, again in scene order. The gradient reaching layer
 // k, d_canvas * prod_{j>k} (1 - w_j) (grad.rs:162-169), is formed as a ratio
@@ -1410,15 +1453,112 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
                                            list[wave], acc, &trans[0][0]);
 }
 
+// fused_kernel with one tile per workgroup (one wave) and no block-level
+// state: each recorded entry's wave sum goes straight into the gradients with
+// float atomics, so a wave needs no accumulator rows, block sums or barriers,
+// and its slot frees as soon as its own tile is done (a block of four waves
+// holds all four until its slowest tile finishes). Slots follow the block order
+// four tiles at a time (tile_geo_wave). Its loss partials are per tile, summed
+// per block in wave order by sum_losses, as the four-wave blocks sum them.
+// Used where fused_kernel would be, outside the deterministic mode.
+template <int MODE, bool FAST>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fused_tile_kernel(RasterArgs a, const float* __restrict__ records,
+                                                                                const TileEnt* __restrict__ ents) {
+    static_assert(MODE == MODE_LOSS || MODE == MODE_GRAD_IN, "gradient modes only");
+    __shared__ uint32_t list[CH];
+    __shared__ __attribute__((aligned(16))) float trans[NP * TP];
+    if (a.halt && *a.halt >= 0) return;
+    const int W = a.W, H = a.H, T = a.T;
+    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B);
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
+    const int lane = tg.lane, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = 1.0f / sig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+
+    Back st;
+    float col[3];
+    for (int ch = 0; ch < 3; ch++) col[ch] = st.col[ch] = a.bg[b * 3 + ch];
+    Trans tot = {1.0f, 0, 0};
+    int n2, rec_chunks;
+    forward_sweep<MODE, FAST, false>(a, rec, tg, validm, rsig, sig, list, col, tot, n2, rec_chunks);
+    if (MODE == MODE_LOSS && a.out_img && tg.valid)
+        for (int ch = 0; ch < 3; ch++) a.out_img[img_index(a, tg.pix, b, ch)] = col[ch];
+    for (int ch = 0; ch < 3; ch++) st.g0[ch] = 0.0f;
+    double l = 0.0;
+    if (tg.valid) {
+        if (MODE == MODE_LOSS) {
+            // the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114) as forward_kernel forms them
+            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            for (int ch = 0; ch < 3; ch++) {
+                float t = a.target[img_index(a, tg.pix, b, ch)];
+                float d = col[ch] - t;
+                l += (double)d * (double)d;
+                st.g0[ch] = scale * (col[ch] - t);
+            }
+        } else {
+            for (int ch = 0; ch < 3; ch++) st.g0[ch] = a.grad_in[img_index(a, tg.pix, b, ch)];
+        }
+    }
+    if (MODE == MODE_LOSS) {
+        l = wave_sum_f64(l);
+        if (lane == 0) a.partial_loss[tg.tile] = l;
+    }
+    // The entries this wave recorded with vector stores are read back below with
+    // scalar loads: the stores are complete (in L2, which the scalar cache reads
+    // from) before any of those loads issue. A tile's region holds whole cache
+    // lines, so no scalar-cache line of it was loaded before its entries were.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    st.tot = tot;
+    st.pre = {1.0f, 0, 0};
+    const bool plain = lane_mask(tot.z != 0 || tot.e != 0) == 0;
+    const int cap2 = a.cap2;
+    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
+    float* const grads = a.grads + (size_t)b * T * NP;
+    lds_float* const tw = (lds_float*)trans;
+    // The recorded entries in scene order (backward_sweep's recorded loop, with
+    // every chunk at once: the gradient rows are global).
+    auto sweep = [&](auto plain_c) {
+        constexpr bool PLAIN = decltype(plain_c)::value;
+        TileEnt nx = te[0];
+        for (int i2 = 0; i2 < n2; i2++) {
+            const TileEnt cur = nx;
+            const int k = (int)(cur.k >> 8);
+            nx = te[min(i2 + 1, cap2 - 1)];
+            const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
+            const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
+            const float* rp = rec + (size_t)k * REC;
+            const Rec r = load_rec(rp);
+            float cov = 1.0f;
+            Geo g;
+            if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            const float w = r.f(R_A) * cov;
+            float part[NP];
+            grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
+            reduce_entry_global(part, tw, grads + (size_t)k * NP, lane);
+        }
+    };
+    if (plain)
+        sweep(std::true_type{});
+    else
+        sweep(std::false_type{});
+}
+
 // The per-item loss (canvas.rs:45-58) from the fused kernel's per-block sums,
 // one wave per scene, in the order of backward_kernel's sum.
-__global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ partial_loss, int nblk, double npix3,
-                                                 float* __restrict__ losses, const int* __restrict__ halt) {
+// per: partials per block, 1 or WAVES (per tile, summed in wave order first).
+__global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ partial_loss, int nblk, int per,
+                                                 double npix3, float* __restrict__ losses,
+                                                 const int* __restrict__ halt) {
     if (halt && *halt >= 0) return;
     const int b = (int)blockIdx.x, lane = (int)threadIdx.x;
-    const double* pl = partial_loss + (size_t)b * nblk;
+    const double* pl = partial_loss + (size_t)b * nblk * per;
     double l = 0.0;
-    for (int r = lane; r < nblk; r += 64) l += pl[r];
+    for (int r = lane; r < nblk; r += 64) {
+        double lb = pl[(size_t)r * per];
+        for (int q = 1; q < per; q++) lb += pl[(size_t)r * per + q];
+        l += lb;
+    }
     l = wave_sum_f64(l);
     if (lane == 0) losses[b] = (float)(l / npix3);
 }
@@ -1701,10 +1841,15 @@ static void launch_fused_d(bool fast, const RasterArgs& a, dim3 grid, hipStream_
 
 template <int MODE>
 static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
-    if (a.deterministic)
+    if (a.deterministic) {
         launch_fused_d<MODE, true>(fast, a, grid, s);
+        return;
+    }
+    const dim3 tiles(grid.x * grid.y * grid.z * WAVES);
+    if (fast)
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
     else
-        launch_fused_d<MODE, false>(fast, a, grid, s);
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
 }
 
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
@@ -1719,10 +1864,10 @@ hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, double npix3, float* losses, hipStream_t s,
-                             const int* halt) {
+hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int per, double npix3, float* losses,
+                             hipStream_t s, const int* halt) {
     if (B == 0) return hipSuccess;
-    hipLaunchKernelGGL(sum_losses, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+    hipLaunchKernelGGL(sum_losses, dim3(B), dim3(64), 0, s, partial_loss, nblk, per, npix3, losses, halt);
     return hipGetLastError();
 }
 

@@ -364,7 +364,8 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
                 "reduce_partials launch");
     } else if (bufs.fused && mode == drh::MODE_LOSS) {
         KernelTimer kt(ctx, TK_REDUCE, s, timed);
-        HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, 3.0 * (double)H * (double)W, out_losses, s, halt),
+        HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, drh::loss_partials_per_block(true, false),
+                                       3.0 * (double)H * (double)W, out_losses, s, halt),
                 "sum_losses launch");
     }
     return DRH_OK;
@@ -405,7 +406,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     if (mode != drh::MODE_RENDER) {
         if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
             return rc;
-        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * sizeof(double), s))) return rc;
+        if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * drh::WAVES * sizeof(double), s))) return rc;  // per tile
         if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
         // the hand-over between the two kernels (the fused kernel keeps it in registers)
         if (!bufs.fused) {

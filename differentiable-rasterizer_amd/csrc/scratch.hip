@@ -55,7 +55,7 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     L.rec = off;
     off = up(off + (size_t)B * T * drh::REC * sizeof(float));
     L.ploss = off;
-    off = up(off + (size_t)B * nblk * sizeof(double));
+    off = up(off + (size_t)B * nblk * drh::WAVES * sizeof(double));  // per tile
     L.pq = off;
     off = up(off + (size_t)B * H * W * sizeof(float));
     L.pg0 = off;
