@@ -849,6 +849,9 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     drh::OrderArgs ord{};
     if (use_order(ctx, a.B, (int)grid.x, (int)grid.y)) ord = {reinterpret_cast<int*>(base + L.ord), (int)grid.x, (int)grid.y};
     a.perm_fwd = a.T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
+    a.gx = (int)grid.x;
+    a.gy = (int)grid.y;
+    a.nseg = 1;
     {
         KernelTimer kt(ctx, TK_SETUP, s);
         const drh::RecordHead head = make_head(B, T, H, W, sigma, flags);
@@ -907,6 +910,9 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     a.tl_n = reinterpret_cast<int*>(const_cast<char*>(base + L.tl_n));
     // the block order the record's setup made (use_order decides alike)
     if (use_order(ctx, a.B, (int)grid.x, (int)grid.y)) a.perm_bwd = reinterpret_cast<const int*>(base + L.ord);
+    a.gx = (int)grid.x;
+    a.gy = (int)grid.y;
+    a.nseg = 1;
     a.grads = grads.dev;
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
