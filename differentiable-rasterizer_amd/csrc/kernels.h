@@ -79,11 +79,15 @@ static_assert(sizeof(TileEnt) == 24, "TileEnt is read as 2 + 4 dwords");
 constexpr int TN_IRREGULAR = 1 << 30;
 
 // The raster kernels' block order, made by setup_records (perm null: none):
-// perm[b * gx*gy + r] is the scene-local index of scene b's r-th heaviest block;
-// gx, gy: blocks per scene row and column, (gx + 1) * (gy + 1) <= ORD_MAX_CELLS.
+// perm[b * gx*gy + r] is the scene-local index of scene b's r-th heaviest cell;
+// gx, gy: cells per scene row and column, (gx + 1) * (gy + 1) <= ORD_MAX_CELLS.
+// A cell is a 16x16 block (shift 4) or, for the one-wave fused kernel, an 8x8
+// tile (shift 3; gx, gy then twice the blocks', so dead tiles of a partial
+// block are cells too).
 struct OrderArgs {
     int* perm;
     int gx, gy;
+    int shift = 4;
 };
 constexpr int ORD_MAX_CELLS = 8192;
 
@@ -109,6 +113,7 @@ struct RasterArgs {
     int chw;               // images, targets and grad_in are B x 3 x H x W (else B x H x W x 3)
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
     const int* perm_bwd;   // block order of the backward kernel or null
+    int perm_tiles;        // perm_bwd orders 8x8 tiles (one-wave fused kernel), not blocks
     const int* halt;       // null, or a flag: every block returns at entry once it is >= 0
     // Split backward (nseg > 1, with a block order): in the nsplit heaviest
     // blocks of each scene, segment s of a tile's recorded entries,

@@ -62,14 +62,14 @@ __device__ inline int upper_bound_px(float hi, float pad, int n) {
     return (c >= (float)n) ? n : (int)c + 1;
 }
 
-// A triangle's cull box in 16x16 blocks (inclusive; x0 > x1 when empty).
+// A triangle's cull box in order cells (inclusive; x0 > x1 when empty).
 struct BlockBox {
     int x0, y0, x1, y1;
 };
 
-// The cull box of triangle p (raster.rs:26-28, 144-168) in 16x16 blocks, for
-// the block-order estimate (a taped forward's liveness: alpha > 0).
-__device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, float sigma) {
+// The cull box of triangle p (raster.rs:26-28, 144-168) in cells of 2^shift
+// pixels, for the block-order estimate (a taped forward's liveness: alpha > 0).
+__device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, float sigma, int shift) {
     float v[6];
     bool finite = true;
     for (int j = 0; j < 6; j++) {
@@ -83,7 +83,7 @@ __device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, 
     const int by0 = lower_bound_px(fminf(fminf(v[1], v[3]), v[5]), pad, H);
     const int bx1 = upper_bound_px(fmaxf(fmaxf(v[0], v[2]), v[4]), pad, W);
     const int by1 = upper_bound_px(fmaxf(fmaxf(v[1], v[3]), v[5]), pad, H);
-    if (bx0 < bx1 && by0 < by1) bb = {bx0 >> 4, by0 >> 4, (bx1 - 1) >> 4, (by1 - 1) >> 4};
+    if (bx0 < bx1 && by0 < by1) bb = {bx0 >> shift, by0 >> shift, (bx1 - 1) >> shift, (by1 - 1) >> shift};
     return bb;
 }
 
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
     for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
     __syncthreads();
     for (int q = threadIdx.x; q < T; q += SETUP_THREADS) {
-        const BlockBox bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma);
+        const BlockBox bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma, o.shift);
         if (bb.x0 <= bb.x1 && bb.y0 <= bb.y1) {
             atomicAdd(&cells[bb.y0 * pitch + bb.x0], 1);
             atomicAdd(&cells[bb.y0 * pitch + bb.x1 + 1], -1);
@@ -838,10 +838,18 @@ __device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int 
 
 // One wave per workgroup, B nb WAVES slots in one dimension: slot i is tile
 // i % WAVES of the block at rank i / (WAVES B) of scene (i / WAVES) % B, so the
-// four tiles of each block by setup_records' order (perm, heaviest first) run
-// in consecutive slots; without perm, block order.
-__device__ inline TileGeo tile_geo_wave(int W, int H, int gx, int gy, const int* perm, int B) {
-    const int nb = gx * gy, i = (int)blockIdx.x, wave = i % WAVES;
+// four tiles of each block by setup_records' block order (perm, heaviest
+// first) run in consecutive slots; without perm, block order.
+// With perm_tiles, perm orders the scene's 2gx x 2gy tiles: slot i is tile
+// rank i / B of scene i % B.
+__device__ inline TileGeo tile_geo_wave(int W, int H, int gx, int gy, const int* perm, int B, bool perm_tiles) {
+    const int nb = gx * gy, i = (int)blockIdx.x;
+    if (perm && perm_tiles) {
+        const int nt = nb * WAVES, b = i % B, rank = i / B;
+        const int t = min(max(perm[(size_t)b * nt + rank], 0), nt - 1), tx = t % (2 * gx), ty = t / (2 * gx);
+        return tile_at(W, H, gx, gy, b, tx >> 1, ty >> 1, rank, 0, 1, (ty & 1) * 2 + (tx & 1));
+    }
+    const int wave = i % WAVES;
     int b, rank, local;
     if (perm) {
         b = (i / WAVES) % B;
@@ -1457,8 +1465,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
 // state: each recorded entry's wave sum goes straight into the gradients with
 // float atomics, so a wave needs no accumulator rows, block sums or barriers,
 // and its slot frees as soon as its own tile is done (a block of four waves
-// holds all four until its slowest tile finishes). Slots follow the block order
-// four tiles at a time (tile_geo_wave). Its loss partials are per tile, summed
+// holds all four until its slowest tile finishes). Slots follow setup_records'
+// order, of tiles (perm_tiles) or of blocks four tiles at a time
+// (tile_geo_wave). Its loss partials are per tile, summed
 // per block in wave order by sum_losses, as the four-wave blocks sum them.
 // Used where fused_kernel would be, outside the deterministic mode.
 template <int MODE, bool FAST>
@@ -1469,7 +1478,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     __shared__ __attribute__((aligned(16))) float trans[NP * TP];
     if (a.halt && *a.halt >= 0) return;
     const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B);
+    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);

@@ -238,6 +238,7 @@ struct RasterBufs {
     float* ckpt = nullptr;          // split backward's checkpoints, or null: no split
     int nseg = 1, seg_m = 0, nsplit = 0;  // its segments, entries per segment, split blocks per scene
     bool fused = false;             // one fused kernel (fused_gradients); pq, pg0, pze, tn unused
+    bool order_tiles = false;       // `order` ranks 8x8 tiles (one-wave fused kernel only), not blocks
 };
 
 // Split of the backward's sweep over a tile's recorded entries. A tile's sweep

@@ -304,7 +304,9 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
     drh::OrderArgs ord{};
-    if (bufs.order) ord = {bufs.order, (int)grid.x, (int)grid.y};
+    if (bufs.order)
+        ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3}
+                               : drh::OrderArgs{bufs.order, (int)grid.x, (int)grid.y, 4};
     {
         KernelTimer kt(ctx, TK_SETUP, s, timed);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
@@ -338,6 +340,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
     a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     a.perm_bwd = ord.perm;
+    a.perm_tiles = bufs.order_tiles ? 1 : 0;
     a.halt = halt;
     a.nseg = bufs.ckpt && ord.perm ? bufs.nseg : 1;
     a.seg_m = bufs.seg_m;
@@ -389,9 +392,9 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     bufs.cap2 = tile_entries(ntiles, (T + 7) & ~7);
     int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
-    if (use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T)) {
-        if ((rc = order.acquire(ctx, K_ORDER, (size_t)B * nblk * sizeof(int), s))) return rc;
-        bufs.order = order.get<int>();
+    const bool ordered =
+        use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T);
+    if (ordered) {
         const int nseg = mode == drh::MODE_RENDER ? 1 : backward_segments(T, bufs.cap2, det, (size_t)B * nblk, ctx->cus);
         if (nseg > 1) {
             const size_t words = ntiles * (size_t)(nseg - 1) * drh::CKPT_WORDS * 64;
@@ -403,6 +406,14 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         }
     }
     bufs.fused = fused_gradients(mode, bufs.nseg, bufs.cap2, T);
+    if (ordered) {
+        // the one-wave fused kernel takes an order of tiles where its cells fit
+        bufs.order_tiles = bufs.fused && !det &&
+                           (size_t)(2 * grid.x + 1) * (2 * grid.y + 1) <= (size_t)drh::ORD_MAX_CELLS;
+        const size_t cells = (size_t)B * nblk * (bufs.order_tiles ? drh::WAVES : 1);
+        if ((rc = order.acquire(ctx, K_ORDER, cells * sizeof(int), s))) return rc;
+        bufs.order = order.get<int>();
+    }
     if (mode != drh::MODE_RENDER) {
         if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
             return rc;
