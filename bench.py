@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: batched soft-raster forward + MSE + backward on one MI355X.
 
-One step = one drh_fused_loss_backward call (setup_records, fused_kernel,
+One step = one drh_fused_loss_backward call (setup_records, fused_tile_kernel,
 sum_losses) over the headline workload: B=16 scenes at 256x256,
 T=128 triangles each, sigma=0.0015, synthetic seeded scenes (diffrast.synth)
 and targets rendered from independently seeded scenes. Inputs and outputs
@@ -9,7 +9,7 @@ stay in HBM; the timed region is K steps between two synchronizations.
 
 Printed (one JSON line on stdout): throughput in dense pixel-triangle
 evaluations per second, ms per batch, the dominant kernel's roofline position
-(fused_kernel: its algorithmic FLOP per launch over its event-timed average
+(fused_tile_kernel: its algorithmic FLOP per launch over its event-timed average
 duration, against the FP32 vector peak; under "two_kernel_path" the same step
 with forward_kernel and backward_kernel, DRH_UNFUSED=1, and their rooflines;
 configurations that take the two kernels report them directly), the CPU
@@ -396,8 +396,8 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
                                       k["forward"] + k["backward"])}
 
     if "fused" in kt:
-        out["roofline"] = roof("fused_kernel", flop_f + flop_b, kt["fused"],
-                               traffic_from_profiles("fused_kernel") if traffic else None)
+        out["roofline"] = roof("fused_tile_kernel", flop_f + flop_b, kt["fused"],
+                               traffic_from_profiles("fused_tile_kernel") if traffic else None)
         two.update(two_kernel_roofs(two["kernel_ms"]))
         two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
         out["two_kernel_path"] = two
