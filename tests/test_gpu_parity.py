@@ -335,6 +335,37 @@ def test_pool_buffers_move_between_streams(ctx):
         assert torch.equal(losses, ref[0]) and torch.equal(grads, ref[1])
 
 
+def test_concurrent_calls_on_one_context(ctx):
+    # The reference's binding lets threads call one device concurrently
+    # (crates/diffrast-py/src/lib.rs:47-65). Four host threads, three
+    # host-array calls each on one context, different scenes per call: every
+    # result equals the same call made alone (fixed-order sums: bit-equal).
+    import threading
+
+    B, H, W, T, sigma = 2, 48, 40, 24, 0.01
+    jobs = [(synth.batch("uniform", B, T, 60 + j),
+             np.stack([synth.blob_target(70 + j * B + b, H, W) for b in range(B)])) for j in range(12)]
+    alone = [ctx.fused_loss_backward(p, t, sigma, deterministic=True) for p, t in jobs]
+    got = [None] * len(jobs)
+    errors = []
+
+    def worker(k):
+        try:
+            for j in range(k, len(jobs), 4):
+                got[j] = ctx.fused_loss_backward(jobs[j][0], jobs[j][1], sigma, deterministic=True)
+        except Exception as e:  # reported below, not swallowed
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for (al, ag), (gl, gg) in zip(alone, got):
+        assert np.array_equal(al, gl) and np.array_equal(ag, gg)
+
+
 def test_adam_step_is_bit_exact(ctx, orc):  # optim.rs:40-60 + fit.rs:399-424
     n = 150
     p0 = synth.uniform_scene(17, 15).ravel().copy()
