@@ -565,17 +565,40 @@ enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 // time, and compacts the entries over them in place. Every branch of the
 // classification is taken by some lane of almost any 64 triangles, so the
 // wave's cost is per pass of 64, and the candidates are usually one pass.
+// The box tests load two passes of 64 triangles at a time (one round trip
+// for both).
+//
+// MERGE (merged chunks): the box tests run on past the first CH triangles
+// until the candidates exceed 64 (so at most 128 = CH, the list's size) or
+// [k0, k1) ends, and *kend is where they stopped: the sparse candidates of
+// many chunks (small triangles) then share one classification pass and one
+// entry loop. Entries then number their triangles from k0 over up to k1 - k0
+// triangles, so only a caller that takes every triangle index from the
+// entries (not from a per-chunk accumulator row) may merge. The
+// classification then also loads every field any of its branches reads up
+// front (one round trip instead of one per branch level; the other callers
+// keep the lazy loads, whose registers their occupancy needs).
+template <bool MERGE = false>
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
-                                 uint32_t* list, int lane, int live) {
+                                 uint32_t* list, int lane, int live, int* kend = nullptr) {
+    static_assert(CH >= 128, "a merged list holds two passes of candidates");
+    static_assert(R_FLAGS == R_BOX + 4, "the box tests read x0 y0 x1 y1 flags as five consecutive ints");
     int nc = 0;
-    for (int base = k0; base < k1; base += 64) {
-        const int k = base + lane;
-        // Lanes past the chunk read its last record (in bounds) and are masked
-        // out; the tests are single-compare lane masks, ANDed as scalars.
-        const int* ri = reinterpret_cast<const int*>(rec + (size_t)min(k, k1 - 1) * REC);
-        const int flags = ri[R_FLAGS];
-        const int bx0 = ri[R_BOX], by0 = ri[R_BOX + 1], bx1 = ri[R_BOX + 2], by1 = ri[R_BOX + 3];
+    if (MERGE) *kend = k1;
+    for (int base2 = k0; base2 < k1; base2 += 128) {
+        int bf[2][5];  // x0 y0 x1 y1 flags of the triangle k of each pass
+        for (int h = 0; h < 2; h++) {
+            // Lanes past the chunk read its last record (in bounds) and are
+            // masked out.
+            const int* ri = reinterpret_cast<const int*>(rec + (size_t)min(base2 + 64 * h + lane, k1 - 1) * REC);
+            for (int f = 0; f < 5; f++) bf[h][f] = ri[R_BOX + f];
+        }
+        for (int h = 0; h < 2; h++) {
+        const int base = base2 + 64 * h, k = base + lane;
+        if (base >= k1) break;
+        const int bx0 = bf[h][0], by0 = bf[h][1], bx1 = bf[h][2], by1 = bf[h][3], flags = bf[h][4];
+        // the tests are single-compare lane masks, ANDed as scalars
         const uint64_t mask = lane_mask(k < k1) & lane_mask((flags & live) != 0) & lane_mask(tx0 < bx1) &
                               lane_mask(bx0 < tx1) & lane_mask(ty0 < by1) & lane_mask(by0 < ty1);
         const bool cand = __builtin_amdgcn_inverse_ballot_w64(mask);
@@ -587,7 +610,13 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
             list[pos] = ((uint32_t)(k - k0) << 1) | (in_box ? 1u : 0u);
         }
         nc += (int)__popcll(mask);
+        if (MERGE && nc > 64) {
+            *kend = min(base + 64, k1);
+            goto classify;
+        }
+        }
     }
+classify:
     // Entry i is written at count + rank <= i, a slot this or an earlier pass
     // has read: the wave's LDS accesses complete in program order.
     int count = 0;
@@ -599,16 +628,31 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
             kl = cd >> 1;
             const float* r = rec + (size_t)(k0 + (int)kl) * REC;
             const int flags = reinterpret_cast<const int*>(r)[R_FLAGS];
+            // With MERGE the classification's fields, [R_N, R_EB), are loaded
+            // together: the empty asm uses them all here, so that the compiler
+            // does not sink each load into the branch that reads it.
+            static_assert(R_OFF == R_N + 6 && R_FAR == R_N + 9 && R_DEEP == R_N + 10 && R_SLACK == R_N + 11 &&
+                              R_D == R_N + 12 && R_SOFF == R_D + 6 && R_LEN == R_D + 9 && R_EB == R_D + 12,
+                          "classification fields: 24 consecutive floats");
+            float cf[24];
+            if (MERGE) {
+                for (int q = 0; q < 24; q++) cf[q] = r[R_N + q];
+                asm volatile("" ::"v"(cf[0]), "v"(cf[1]), "v"(cf[2]), "v"(cf[3]), "v"(cf[4]), "v"(cf[5]),
+                             "v"(cf[6]), "v"(cf[7]), "v"(cf[8]), "v"(cf[9]), "v"(cf[10]), "v"(cf[11]), "v"(flags));
+                asm volatile("" ::"v"(cf[12]), "v"(cf[13]), "v"(cf[14]), "v"(cf[15]), "v"(cf[16]), "v"(cf[17]),
+                             "v"(cf[18]), "v"(cf[19]), "v"(cf[20]), "v"(cf[21]), "v"(cf[22]), "v"(cf[23]));
+            }
+            auto fld = [&](int i) { return MERGE ? cf[i - R_N] : r[i]; };
             {
                 cls = CLS_PARTIAL;
                 const bool in_box = cd & 1u;
                 if (in_box) extra |= ENT_INBOX;
                 if (flags & F_FAST) {
-                    float far = r[R_FAR], deep = r[R_DEEP];
+                    float far = fld(R_FAR), deep = fld(R_DEEP);
                     float lmin[3], lmax[3];
                     bool culled = false, all_deep = true;
                     for (int j = 0; j < 3; j++) {
-                        float nx = r[R_N + 2 * j], ny = r[R_N + 2 * j + 1], o = r[R_OFF + j];
+                        float nx = fld(R_N + 2 * j), ny = fld(R_N + 2 * j + 1), o = fld(R_OFF + j);
                         float l00 = fmaf(cx0, nx, fmaf(cy0, ny, -o));
                         float l10 = fmaf(cx1, nx, fmaf(cy0, ny, -o));
                         float l01 = fmaf(cx0, nx, fmaf(cy1, ny, -o));
@@ -623,11 +667,11 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                     } else if (all_deep && in_box) {
                         cls = CLS_FULL;
                     } else {
-                        const float slack = r[R_SLACK];
+                        const float slack = fld(R_SLACK);
                         float lb[3], ubmin = INFINITY;
                         for (int j = 0; j < 3; j++) {
-                            float dx = r[R_D + 2 * j], dy = r[R_D + 2 * j + 1], so = r[R_SOFF + j];
-                            float len = r[R_LEN + j];
+                            float dx = fld(R_D + 2 * j), dy = fld(R_D + 2 * j + 1), so = fld(R_SOFF + j);
+                            float len = fld(R_LEN + j);
                             float s00 = fmaf(cx0, dx, fmaf(cy0, dy, -so));
                             float s10 = fmaf(cx1, dx, fmaf(cy0, dy, -so));
                             float s01 = fmaf(cx0, dx, fmaf(cy1, dy, -so));
@@ -896,8 +940,10 @@ __device__ inline TileGeo tile_geo_split(int W, int H, int gx, int gy, const int
 // the gradient modes, multiplies the taped transmittance into tot (which comes
 // in as an empty product) and records the tile's contributing entries: n2 of
 // them seen, those of the first rec_chunks chunks all recorded. With CKPT, the
-// split backward's checkpoints too. lw: the wave's LDS list.
-template <int MODE, bool FAST, bool CKPT>
+// split backward's checkpoints too. lw: the wave's LDS list. MERGE: lists of
+// merged chunks (build_list), for a caller that takes every triangle index from
+// the recorded entries; rec_chunks is then meaningless.
+template <int MODE, bool FAST, bool CKPT, bool MERGE = false>
 __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* __restrict__ rec, const TileGeo& tg,
                                               uint64_t validm, float rsig, float sig, uint32_t* lw,
                                               float (&col)[3], Trans& tot, int& n2, int& rec_chunks) {
@@ -917,10 +963,13 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
     int ck = 0, ck_at = nck > 0 ? a.seg_m : INT_MAX;
     float* ckw = nck > 0 ? a.ckpt + (size_t)uniform_u32((uint32_t)tg.tile) * nck * (CKPT_WORDS * 64) : nullptr;
 
-    for (int c = 0; c < n_chunks; c++) {
-        int k0 = c * CH, k1 = min(T, k0 + CH);
-        int count = tg.live ? build_list(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0, tg.cx1,
-                                         tg.cy1, lw, lane, F_LIVE)
+    static_assert(!(MERGE && CKPT), "checkpoints count entries per chunk");
+    int k1 = 0;
+    for (int c = 0; MERGE ? k1 < T : c < n_chunks; c++) {
+        const int k0 = MERGE ? k1 : c * CH;
+        k1 = MERGE ? T : min(T, k0 + CH);
+        int count = tg.live ? build_list<MERGE>(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
+                                                tg.cx1, tg.cy1, lw, lane, F_LIVE, &k1)
                             : 0;
         uint32_t nxt = lw[0];  // the next entry is read one iteration ahead
         for (int i = 0; i < count; i++) {
@@ -1490,7 +1539,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     for (int ch = 0; ch < 3; ch++) col[ch] = st.col[ch] = a.bg[b * 3 + ch];
     Trans tot = {1.0f, 0, 0};
     int n2, rec_chunks;
-    forward_sweep<MODE, FAST, false>(a, rec, tg, validm, rsig, sig, list, col, tot, n2, rec_chunks);
+    // merged chunks: the sweep below reads each entry's triangle index
+    forward_sweep<MODE, FAST, false, true>(a, rec, tg, validm, rsig, sig, list, col, tot, n2, rec_chunks);
     if (MODE == MODE_LOSS && a.out_img && tg.valid)
         for (int ch = 0; ch < 3; ch++) a.out_img[img_index(a, tg.pix, b, ch)] = col[ch];
     for (int ch = 0; ch < 3; ch++) st.g0[ch] = 0.0f;
