@@ -1,6 +1,8 @@
 // Shared definitions between the HIP kernels and the host runtime.
 #pragma once
 
+#include <cmath>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -94,6 +96,10 @@ constexpr int ORD_MAX_CELLS = 8192;
 struct RasterArgs {
     int B, T, H, W;
     float sigma;
+    // Wave-uniform quotients, divided once on the host (IEEE, as the kernels
+    // would): rsig = 1 / max(sigma, 1e-8), lscale = 2 / (3 H W) (dL/dpixel).
+    // Set with set_sizes, which also fills B, T, H, W and sigma.
+    float rsig, lscale;
     const float* rec;      // B*T*REC
     const float* bg;       // B*3
     const float* target;   // B*H*W*3 (MODE_LOSS)
@@ -126,6 +132,16 @@ struct RasterArgs {
     int gx, gy;            // blocks per scene row and column
     float* ckpt;           // ntiles * (nseg - 1) * CKPT_WORDS * 64
 };
+
+inline void set_sizes(RasterArgs& a, int B, int T, int H, int W, float sigma) {
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    a.W = W;
+    a.sigma = sigma;
+    a.rsig = 1.0f / std::fmax(sigma, 1e-8f);
+    a.lscale = 2.0f / (float)(3 * (size_t)W * H);
+}
 
 // A checkpoint word per lane: colour (3), transmittance q, zero count z and
 // rescaling count e (as int bits).

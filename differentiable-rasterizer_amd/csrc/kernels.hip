@@ -87,6 +87,95 @@ __device__ inline BlockBox block_box(const float* __restrict__ p, int W, int H, 
     return bb;
 }
 
+// The order estimate of one triangle: which cells it can reach. Its cull box
+// in cells, `far` (the distance beyond which its weight is below MIN_WEIGHT:
+// alpha sigmoid(-d / sigma) < alpha e^(-d / sigma)), and its vertices sorted
+// by y (top t, middle m, bottom b) with the slopes dx/dy of the long edge tb
+// and the short edges tm and mb. Made once per triangle and kept in LDS for
+// the threads that walk its cell rows. The arithmetic is approximate: the
+// estimate only orders the cells.
+struct Reach {
+    float xt, yt, xm, ym, xb, yb, s_tb, s_tm, s_mb, far;
+    uint32_t lo, hi;  // cull box in cells: x0 | y0 << 16, x1 | y1 << 16 (x0 > x1 when culled)
+    __device__ int x0() const { return (int)(lo & 0xFFFFu); }
+    __device__ int y0() const { return (int)(lo >> 16); }
+    __device__ int x1() const { return (int)(hi & 0xFFFFu); }
+    __device__ int y1() const { return (int)(hi >> 16); }
+};
+static_assert(ORD_MAX_CELLS <= 0xFFFF, "cell indices fit 16 bits");
+
+__device__ inline float slope(float dx, float dy) { return dy > 0.0f ? __fdividef(dx, dy) : 0.0f; }
+
+__device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sigma, int shift) {
+    Reach r;
+    const BlockBox bb = block_box(p, W, H, sigma, shift);  // finite vertices, alpha > 0
+    r.lo = 1u | 1u << 16;  // culled
+    r.hi = 0u;
+    if (bb.x0 > bb.x1 || bb.y0 > bb.y1) return r;
+    r.lo = (uint32_t)bb.x0 | (uint32_t)bb.y0 << 16;
+    r.hi = (uint32_t)bb.x1 | (uint32_t)bb.y1 << 16;
+    r.far = fmaxf(__logf(fminf(p[9], 1.0f) * (1.0f / MIN_WEIGHT)) + 0.05f, 0.0f) * fmaxf(sigma, 1e-8f);
+    float ax = p[0], ay = p[1], bx = p[2], by = p[3], cx = p[4], cy = p[5];
+    auto order = [](float& ux, float& uy, float& vx, float& vy) {
+        if (vy < uy) {
+            const float tx = ux, ty = uy;
+            ux = vx;
+            uy = vy;
+            vx = tx;
+            vy = ty;
+        }
+    };
+    order(ax, ay, bx, by);
+    order(bx, by, cx, cy);
+    order(ax, ay, bx, by);
+    r.xt = ax;
+    r.yt = ay;
+    r.xm = bx;
+    r.ym = by;
+    r.xb = cx;
+    r.yb = cy;
+    r.s_tb = slope(cx - ax, cy - ay);
+    r.s_tm = slope(bx - ax, by - ay);
+    r.s_mb = slope(cx - bx, cy - by);
+    return r;
+}
+
+// Counts the cells the triangle can reach into the difference rows `cells`
+// (pitch ints per cell row), for cell rows j, j + m, ... of its cull box: in
+// each row, the run of cells whose pixel centres come within `far` of the
+// triangle. The run is the triangle's x extent inside the cell row's band of
+// pixel centres widened by `far` (the edges' x at the band's clipped ends, and
+// the vertices inside it), widened by `far` in x and clipped to the cull box.
+// It over-counts cells near the triangle's corners a little; a count of the
+// cull box alone also counts the cells between a thin or slanted triangle's
+// edges and its box, which are often most of them. r is taken by value: its
+// fields stay in registers over the rows.
+__device__ inline void reach_rows(const Reach r, int W, int H, int shift, int j, int m, int* cells, int pitch) {
+    const float cs = (float)(1 << shift), rH = 1.0f / (float)H, cell_h = cs * rH, wc = (float)W / cs;
+    const float band = (cs - 1.0f) * rH + 2.0f * r.far, y_first = 0.5f * rH - r.far;
+    const float c0_off = (0.5f - cs) / cs, c1_off = -0.5f / cs;
+    auto short_x = [&](float y) { return y <= r.ym ? fmaf(y - r.yt, r.s_tm, r.xt) : fmaf(y - r.ym, r.s_mb, r.xm); };
+    const int x0 = r.x0(), x1 = r.x1(), y1 = r.y1();
+    for (int y = r.y0() + j; y <= y1; y += m) {
+        const float ya = fmaf((float)y, cell_h, y_first);
+        const float ca = fmaxf(ya, r.yt), cb = fminf(ya + band, r.yb);
+        if (!(ca <= cb)) continue;
+        const float la = fmaf(ca - r.yt, r.s_tb, r.xt), lb = fmaf(cb - r.yt, r.s_tb, r.xt);
+        const float sa = short_x(ca), sb = short_x(cb);
+        float lo = fminf(fminf(la, lb), fminf(sa, sb)), hi = fmaxf(fmaxf(la, lb), fmaxf(sa, sb));
+        const bool mid = ca <= r.ym && r.ym <= cb, bot = ca <= r.yb && r.yb <= cb;
+        lo = fminf(lo, fminf(mid ? r.xm : lo, bot ? r.xb : lo));
+        hi = fmaxf(hi, fmaxf(mid ? r.xm : hi, bot ? r.xb : hi));
+        // cells c whose centres (c cs + 0.5) / W .. (c cs + cs - 0.5) / W meet [lo - far, hi + far]
+        const float c0f = ceilf(fmaf(lo - r.far, wc, c0_off)), c1f = floorf(fmaf(hi + r.far, wc, c1_off));
+        const int c0 = (int)fminf(fmaxf(c0f, (float)x0), (float)(x1 + 1));
+        const int c1 = (int)fmaxf(fminf(c1f, (float)x1), (float)(x0 - 1));
+        if (c0 > c1) continue;
+        atomicAdd(&cells[y * pitch + c0], 1);
+        atomicAdd(&cells[y * pitch + c1 + 1], -1);
+    }
+}
+
 // Setup of triangle i (scene-major index): its record.
 __device__ inline void setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
                                  int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
@@ -209,60 +298,73 @@ __device__ inline void setup_one(const float* __restrict__ params, size_t i, int
 // The raster kernels' block order, heaviest first. A block's time follows its
 // tiles' lists; the longest blocks, started late in a grid of several rounds,
 // run on while most of the device has nothing left, and heavy blocks that land
-// on one CU finish last. A block's cost is estimated by the number of triangle
-// boxes that overlap it plus a share for building its lists (which reads every
-// triangle). Each scene's workgroup counts the overlaps in LDS (a 2D difference
-// grid: four adds per triangle, then prefix sums along rows and columns),
-// counting-sorts the scene's blocks by the estimate, heaviest first, and writes
-// their scene-local indices to perm[b * nb ...]. The raster kernels take launch
+// on one CU finish last. A block's cost is estimated by the number of
+// triangles that can reach it (reach_rows) plus a share for building its lists
+// (which reads every triangle). Each scene's workgroup counts them in LDS (a
+// difference array per cell row: two adds per triangle and row, then prefix
+// sums along the rows), counting-sorts the scene's blocks by the estimate,
+// heaviest first, and writes their scene-local indices to perm[b * nb ...]. The raster kernels take launch
 // slot i to rank i / B of scene i % B, so the heaviest blocks of every scene go
 // first. Nothing crosses workgroups: a device-wide hand-off would cost more
 // than the order saves.
-constexpr int SETUP_THREADS = 256, ORD_BUCKETS = 1024;
+constexpr int SETUP_THREADS = 1024, ORD_BUCKETS = 1024, ORD_REACH = 512;
+static_assert(ORD_BUCKETS % SETUP_THREADS == 0 && SETUP_THREADS % 64 == 0, "order workgroup shape");
+
+// Inclusive prefix sum over the wave's lanes (every lane active).
+// DPP row shifts within each row of 16 lanes (lanes with no source read the
+// `old` operand, 0), then the last lane of rows 0 and 2 broadcast into rows 1
+// and 3, then lane 31 into rows 2 and 3 (gfx9 row_bcast).
+__device__ inline int wave_scan_incl(int v, int) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
 
 __device__ inline void order_scene(const OrderArgs& o, int* cells, int b, int T) {
+    static_assert(ORD_BUCKETS == SETUP_THREADS && SETUP_THREADS / 64 <= 64, "one bucket per thread");
     __shared__ int hist[ORD_BUCKETS];
-    __shared__ int scan[SETUP_THREADS];
-    const int t = threadIdx.x, gx = o.gx, gy = o.gy, pitch = gx + 1, nb = gx * gy;
-    for (int y = t; y <= gy; y += SETUP_THREADS) {
-        int run = 0;
-        for (int x = 0; x <= gx; x++) run = (cells[y * pitch + x] += run);
+    __shared__ int wsum[SETUP_THREADS / 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gx = o.gx, gy = o.gy, pitch = gx + 1, nb = gx * gy;
+    // prefix sums along the cell rows, one wave per row at a time: 64 cells per
+    // step, a wave scan plus the carry of the row's earlier cells
+    for (int y = wave; y < gy; y += SETUP_THREADS / 64) {
+        int carry = 0;
+        for (int x0 = 0; x0 <= gx; x0 += 64) {
+            const int x = x0 + lane;
+            const int v = wave_scan_incl(x <= gx ? cells[y * pitch + x] : 0, lane);
+            if (x <= gx) cells[y * pitch + x] = v + carry;
+            carry += __shfl(v, 63, 64);
+        }
     }
-    for (int k = t; k < ORD_BUCKETS; k += SETUP_THREADS) hist[k] = 0;
+    hist[t] = 0;
     __syncthreads();
-    for (int x = t; x <= gx; x += SETUP_THREADS) {
-        int run = 0;
-        for (int y = 0; y <= gy; y++) run = (cells[y * pitch + x] += run);
-    }
-    __syncthreads();
-    const int base = 6 * ((T + 63) / 64);  // list building, against one overlapping box
+    const int base = 6 * ((T + 63) / 64);  // list building, against one reaching triangle
     auto key = [&](int blk) {
         const int c = cells[(blk / gx) * pitch + blk % gx] + base;
         return ORD_BUCKETS - 1 - min(c, ORD_BUCKETS - 1);
     };
     for (int blk = t; blk < nb; blk += SETUP_THREADS) atomicAdd(&hist[key(blk)], 1);
     __syncthreads();
-    // exclusive prefix of the histogram: four buckets per thread, then a scan of
-    // the partial sums (Hillis-Steele in place)
-    constexpr int PER = ORD_BUCKETS / SETUP_THREADS;
-    int part = 0;
-    for (int q = 0; q < PER; q++) part += hist[t * PER + q];
-    scan[t] = part;
+    // exclusive prefix of the histogram: a scan in each wave, then of the
+    // waves' totals
+    const int own = hist[t], incl = wave_scan_incl(own, lane);
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    for (int off = 1; off < SETUP_THREADS; off <<= 1) {
-        const int add = t >= off ? scan[t - off] : 0;
-        __syncthreads();
-        scan[t] += add;
-        __syncthreads();
-    }
-    int run = scan[t] - part;
-    for (int q = 0; q < PER; q++) {
-        const int c = hist[t * PER + q];
-        hist[t * PER + q] = run;
-        run += c;
+    if (wave == 0) {
+        const int w = wave_scan_incl(lane < SETUP_THREADS / 64 ? wsum[lane] : 0, lane);
+        if (lane < SETUP_THREADS / 64) wsum[lane] = w;
     }
     __syncthreads();
-    for (int blk = t; blk < nb; blk += SETUP_THREADS) o.perm[(size_t)b * nb + atomicAdd(&hist[key(blk)], 1)] = blk;
+    hist[t] = incl - own + (wave > 0 ? wsum[wave - 1] : 0);
+    __syncthreads();
+    for (int blk = t; blk < nb; blk += SETUP_THREADS) {
+        const int pos = atomicAdd(&hist[key(blk)], 1);  // < nb: the offsets partition [0, nb)
+        if (pos < nb) o.perm[(size_t)b * nb + pos] = blk;
+    }
 }
 
 // Workgroup (x, b) with x < nrec = ceil(T / n), n the workgroup size: the
@@ -289,18 +391,30 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
         if (k < T) setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
         return;
     }
+    // Triangles in batches of up to ORD_REACH: each one's Reach made by one
+    // thread into LDS, then its cell rows walked by m threads (when the batch
+    // leaves threads over), each taking every m-th row. A batch's parameters
+    // are loaded before the work that precedes its Reach (the first batch's
+    // before the cells are cleared).
+    __shared__ Reach reach[ORD_REACH];
+    float pk[NP];
+    auto load_batch = [&](int k0) {
+        const int k = k0 + (int)threadIdx.x;
+        if ((int)threadIdx.x < ORD_REACH && k < T)
+            for (int q = 0; q < NP; q++) pk[q] = params[((size_t)b * T + k) * NP + q];
+    };
+    load_batch(0);
     for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
-    __syncthreads();
-    for (int q = threadIdx.x; q < T; q += SETUP_THREADS) {
-        const BlockBox bb = block_box(params + ((size_t)b * T + q) * NP, W, H, sigma, o.shift);
-        if (bb.x0 <= bb.x1 && bb.y0 <= bb.y1) {
-            atomicAdd(&cells[bb.y0 * pitch + bb.x0], 1);
-            atomicAdd(&cells[bb.y0 * pitch + bb.x1 + 1], -1);
-            atomicAdd(&cells[(bb.y1 + 1) * pitch + bb.x0], -1);
-            atomicAdd(&cells[(bb.y1 + 1) * pitch + bb.x1 + 1], 1);
-        }
+    for (int k0 = 0; k0 < T; k0 += ORD_REACH) {
+        const int nt = min(ORD_REACH, T - k0);
+        if ((int)threadIdx.x < nt) reach[threadIdx.x] = make_reach(pk, W, H, sigma, o.shift);
+        load_batch(k0 + ORD_REACH);
+        __syncthreads();
+        const int m = min(SETUP_THREADS / nt, 16);
+        for (int w = threadIdx.x; w < nt * m; w += SETUP_THREADS)
+            reach_rows(reach[w / m], W, H, o.shift, w % m, m, cells, pitch);
+        __syncthreads();
     }
-    __syncthreads();
     order_scene(o, cells, b, T);
 }
 
@@ -1049,7 +1163,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
+    const float rsig = a.rsig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
 
     float col[3];
@@ -1081,7 +1195,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(8)))
     if (MODE == MODE_LOSS) {
         double l = 0.0;
         if (tg.valid) {
-            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            const float scale = a.lscale;
             for (int ch = 0; ch < 3; ch++) {
                 float t = a.target[img_index(a, tg.pix, b, ch)];
                 float d = col[ch] - t;
@@ -1375,7 +1489,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(REBU
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
+    const float rsig = a.rsig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
 
     const int n2r = (int)uniform_u32((uint32_t)a.tl_n[2 * tg.tile]);
@@ -1461,7 +1575,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, wave = tg.wave, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
+    const float rsig = a.rsig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
 
     Back st;
@@ -1477,7 +1591,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
     if (tg.valid) {
         if (MODE == MODE_LOSS) {
             // the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114) as forward_kernel forms them
-            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            const float scale = a.lscale;
             for (int ch = 0; ch < 3; ch++) {
                 float t = a.target[img_index(a, tg.pix, b, ch)];
                 float d = col[ch] - t;
@@ -1531,7 +1645,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
-    const float rsig = 1.0f / sig;
+    const float rsig = a.rsig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
 
     Back st;
@@ -1548,7 +1662,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     if (tg.valid) {
         if (MODE == MODE_LOSS) {
             // the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114) as forward_kernel forms them
-            float scale = 2.0f / (float)(3 * (size_t)W * H);
+            const float scale = a.lscale;
             for (int ch = 0; ch < 3; ch++) {
                 float t = a.target[img_index(a, tg.pix, b, ch)];
                 float d = col[ch] - t;

@@ -316,11 +316,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
                 "setup_records launch");
     }
     drh::RasterArgs a{};
-    a.B = B;
-    a.T = T;
-    a.H = H;
-    a.W = W;
-    a.sigma = sigma;
+    drh::set_sizes(a, B, T, H, W, sigma);
     a.rec = bufs.rec;
     a.bg = bgs;
     a.target = mode == drh::MODE_LOSS ? img_in : nullptr;
@@ -842,11 +838,7 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     if ((rc = stage_out(ctx, img, K_OUT_IMAGES, out_images, (size_t)B * H * W * 3, host, s))) return rc;
     char* base = static_cast<char*>(record);
     drh::RasterArgs a{};
-    a.B = (int)B;
-    a.T = (int)T;
-    a.H = (int)H;
-    a.W = (int)W;
-    a.sigma = sigma;
+    drh::set_sizes(a, (int)B, (int)T, (int)H, (int)W, sigma);
     a.rec = reinterpret_cast<float*>(base + L.rec);
     a.bg = reinterpret_cast<float*>(base + L.bg);
     a.out_img = img.dev;
@@ -904,11 +896,7 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s))) return rc;
     const char* base = static_cast<const char*>(record);
     drh::RasterArgs a{};
-    a.B = (int)B;
-    a.T = (int)T;
-    a.H = (int)H;
-    a.W = (int)W;
-    a.sigma = sigma;
+    drh::set_sizes(a, (int)B, (int)T, (int)H, (int)W, sigma);
     a.rec = reinterpret_cast<const float*>(base + L.rec);
     a.bg = reinterpret_cast<const float*>(base + L.bg);
     a.grad_in = gi.dev;
