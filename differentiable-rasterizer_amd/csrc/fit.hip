@@ -1,15 +1,16 @@
 // The fit loop (crates/diffrast/src/fit.rs:166-335) behind the C ABI: a
 // step-wise fitter whose state lives on the device, and drh_fit on top of it.
 //
-// Every iteration is setup_records -> forward_kernel -> backward_kernel ->
-// reduce_partials (fixed-order sums, so a fit with a given start is
-// reproducible like the reference's, fit.rs:487-496) -> fit_tail, which does
+// Every iteration is setup_records -> the deterministic raster kernels ->
+// fit_step, which sums the partial rows in a fixed order (so a fit with a
+// given start is reproducible like the reference's, fit.rs:487-496) and does
 // the bookkeeping of fit.rs:243-288 on the device: divergence stop before the
 // optimizer sees the loss, loss record, best snapshot taken before the update,
-// patience, then Adam and the projection. Once fit_tail has stopped the fit,
-// every kernel of a later iteration returns at entry (the `halt` flag is the
-// device state's stop field), so iterations launched ahead of a host check do
-// no work.
+// patience, then Adam and the projection. The device state is double-buffered
+// by iteration parity (iteration i reads state i & 1 and writes the other).
+// Once fit_step has stopped the fit, every kernel of a later iteration returns
+// at entry (the `halt` flag mirrors the stop code) and fit_step only carries
+// the state forward, so iterations launched ahead of a host check do no work.
 
 #include <hip/hip_runtime.h>
 
@@ -36,9 +37,11 @@ struct drh_fitter {
     float *losses = nullptr, *loss = nullptr;
     // images: the target (H x W x 3) and the background (3)
     float *target = nullptr, *bg = nullptr;
-    drh::FitState* st = nullptr;
+    drh::FitState* st = nullptr;  // two states, by iteration parity
+    int* halt = nullptr;          // the stop code once stopped, else -1
     drh::FitState last{};   // the device state as last read back
     int64_t next = 0;       // index of the next iteration to launch
+    int64_t launched = 0;   // iterations launched (the latest state is st[launched & 1])
     bool stopped = false;   // Fitter::stop_reason.is_some()
     int stop_reason = DRH_STOP_COMPLETED;
 };
@@ -46,6 +49,12 @@ struct drh_fitter {
 namespace {
 
 constexpr float BETA1 = 0.9f, BETA2 = 0.999f, EPS = 1e-8f;  // optim.rs:29-31
+
+// The fitter's device state: the bookkeeping by iteration parity and the halt flag.
+struct FitDevState {
+    drh::FitState st[2];
+    int halt;
+};
 constexpr int64_t POLL_EVERY = 64;  // drh_fitter_run reads the device state this often
 
 // fit.rs:343-349
@@ -59,22 +68,37 @@ float sigma_at(const drh_fit_config& c, int64_t i) {
 int launch_iteration(drh_fitter* f, int64_t i) {
     const float sigma = sigma_at(f->cfg, i);
     const uint32_t flags = f->math | DRH_DETERMINISTIC;
-    const int* halt = &f->st->stop;
-    int rc = run_raster(f->ctx, drh::MODE_LOSS, f->params, f->bg, f->target, 1, f->T, f->H, f->W, sigma, nullptr,
-                        f->grads, f->loss, flags, f->s, halt);
-    if (rc) return rc;
     const int32_t t = (int32_t)(i + 1);  // Adam's step count after its increment (optim.rs:41)
-    const float bc1 = 1.0f - powi_f32(BETA1, t), bc2 = 1.0f - powi_f32(BETA2, t);
-    KernelTimer kt(f->ctx, TK_ADAM, f->s);
-    HIP_TRY(drh::launch_fit_tail((int)i, f->loss, f->params, f->grads, f->m, f->v, f->lr, f->T * NP, BETA1, BETA2,
-                                 EPS, bc1, bc2, f->cfg.min_delta, f->cfg.patience, f->st, f->losses, f->best, f->s),
-            "fit_tail launch");
+    drh::FitTail tail{};
+    tail.iter = (int)i;
+    tail.loss = f->loss;
+    tail.params = f->params;
+    tail.grads = f->grads;
+    tail.m = f->m;
+    tail.v = f->v;
+    tail.lr = f->lr;
+    tail.beta1 = BETA1;
+    tail.beta2 = BETA2;
+    tail.eps = EPS;
+    tail.bc1 = 1.0f - powi_f32(BETA1, t);
+    tail.bc2 = 1.0f - powi_f32(BETA2, t);
+    tail.min_delta = f->cfg.min_delta;
+    tail.patience = f->cfg.patience;
+    tail.st = f->st;
+    tail.halt = f->halt;
+    tail.losses_out = f->losses;
+    tail.best = f->best;
+    int rc = run_raster(f->ctx, drh::MODE_LOSS, f->params, f->bg, f->target, 1, f->T, f->H, f->W, sigma, nullptr,
+                        f->grads, f->loss, flags, f->s, f->halt, &tail);
+    if (rc) return rc;
+    f->launched = i + 1;
     return DRH_OK;
 }
 
 // Reads the device state (and, when `loss` is given, the last loss) back.
 int read_state(drh_fitter* f, float* loss = nullptr) {
-    HIP_TRY(hipMemcpyAsync(&f->last, f->st, sizeof f->last, hipMemcpyDeviceToHost, f->s), "read fit state");
+    HIP_TRY(hipMemcpyAsync(&f->last, f->st + (f->launched & 1), sizeof f->last, hipMemcpyDeviceToHost, f->s),
+            "read fit state");
     if (loss) HIP_TRY(hipMemcpyAsync(loss, f->loss, sizeof(float), hipMemcpyDeviceToHost, f->s), "read loss");
     int rc = wait_stream(f->s);
     if (rc) return rc;
@@ -146,7 +170,7 @@ int drh_fitter_create(drh_ctx* ctx, const float* target, int64_t H, int64_t W, c
         return code;
     };
     if ((rc = f->work.acquire(ctx, K_FIT_F32, (n * 6 + iters + 1) * sizeof(float), f->s))) return bail(rc);
-    if ((rc = f->state.acquire(ctx, K_FIT_STATE, sizeof(drh::FitState), f->s))) return bail(rc);
+    if ((rc = f->state.acquire(ctx, K_FIT_STATE, sizeof(FitDevState), f->s))) return bail(rc);
     if ((rc = f->images.acquire(ctx, K_FIT_TARGET, (npix3 + 3) * sizeof(float), f->s))) return bail(rc);
     f->params = f->work.get<float>();
     f->m = f->params + n;
@@ -158,7 +182,8 @@ int drh_fitter_create(drh_ctx* ctx, const float* target, int64_t H, int64_t W, c
     f->loss = f->losses + iters;
     f->target = f->images.get<float>();
     f->bg = f->target + npix3;
-    f->st = f->state.get<drh::FitState>();
+    f->st = f->state.get<FitDevState>()->st;
+    f->halt = &f->state.get<FitDevState>()->halt;
 
     // fit.rs:388-396 learning_rates()
     std::vector<float> lr(n);
@@ -168,6 +193,7 @@ int drh_fitter_create(drh_ctx* ctx, const float* target, int64_t H, int64_t W, c
         lr[k * NP + 9] = cfg->lr_alpha;
     }
     const drh::FitState st0{INFINITY, 0, 0, 0, -1};
+    const FitDevState dev0{{st0, st0}, -1};
     const hipMemcpyKind in = host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
     auto copy = [&](void* dst, const void* src, size_t bytes, hipMemcpyKind k) {
         return hipMemcpyAsync(dst, src, bytes, k, f->s);
@@ -177,10 +203,10 @@ int drh_fitter_create(drh_ctx* ctx, const float* target, int64_t H, int64_t W, c
     if (e == hipSuccess) e = copy(f->target, target, npix3 * sizeof(float), in);
     if (e == hipSuccess) e = copy(f->bg, background, 3 * sizeof(float), in);
     if (e == hipSuccess) e = copy(f->lr, lr.data(), n * sizeof(float), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = copy(f->st, &st0, sizeof st0, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = copy(f->state.get<FitDevState>(), &dev0, sizeof dev0, hipMemcpyHostToDevice);
     if (e != hipSuccess) return bail(hip_fail(e, "fitter set-up copies"));
     if ((e = drh::launch_zero(f->m, 2 * n, f->s)) != hipSuccess) return bail(hip_fail(e, "zero moments"));
-    // lr and st0 are host stack memory: wait before they go
+    // lr and dev0 are host stack memory: wait before they go
     if ((rc = wait_stream(f->s))) return bail(rc);
     f->last = st0;
     *out = f;

@@ -168,12 +168,26 @@ struct FitState {
     int stop;  // -1 while running, else STOP_*
 };
 
-dim3 raster_grid(int B, int W, int H);
-hipError_t launch_fit_tail(int iter, const float* loss, float* params, const float* grads, float* m, float* v,
-                           const float* lr, int n, float beta1, float beta2, float eps, float bc1, float bc2,
-                           float min_delta, long long patience, FitState* st, float* losses_out,
-                           float* best_params, hipStream_t s);
+// The fit loop's step after the deterministic raster kernels (fit_step): the
+// partial rows' reduction, the fit bookkeeping and Adam with the projection.
+// The state is double-buffered by iteration parity: iteration i reads st[i & 1]
+// and its first block writes st[(i + 1) & 1], so every block decides from the
+// same state; `halt` mirrors the stop code for the next iterations' kernels.
+struct FitTail {
+    int iter;
+    float* loss;  // the iteration's loss (1 float)
+    float *params, *grads, *m, *v;
+    const float* lr;
+    float beta1, beta2, eps, bc1, bc2, min_delta;
+    long long patience;
+    FitState* st;  // 2 states
+    int* halt;
+    float *losses_out, *best;
+};
 
+dim3 raster_grid(int B, int W, int H);
+hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int T, double npix3,
+                           const FitTail& ft, hipStream_t s);
 // bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src; with
 // o.cnt, the block order is made (OrderArgs).
 // halt (optional): the kernel does nothing once *halt >= 0 (a stopped fit).

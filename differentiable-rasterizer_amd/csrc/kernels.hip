@@ -1805,60 +1805,100 @@ __global__ void adam_project(float* __restrict__ params, const float* __restrict
     params[i] = pv;
 }
 
-// One fit iteration's bookkeeping and update (fit.rs:243-288), after the loss
-// of iteration `iter` has been reduced into loss[0]. One block: thread 0
-// decides (divergence, record, best, patience), then all threads snapshot the
-// best scene before the update and apply Adam + projection.
-__global__ __launch_bounds__(256) void fit_tail(int iter, const float* __restrict__ loss,
-                                                float* __restrict__ params, const float* __restrict__ grads,
-                                                float* __restrict__ m, float* __restrict__ v,
-                                                const float* __restrict__ lr, int n, float beta1, float beta2,
-                                                float eps, float bc1, float bc2, float min_delta,
-                                                long long patience, FitState* __restrict__ st,
-                                                float* __restrict__ losses_out, float* __restrict__ best_params) {
+// The fit loop's iteration tail in one kernel (B = 1): reduce_partials' sums,
+// then the iteration's bookkeeping (fit.rs:243-288: divergence, loss record,
+// best, patience), the best snapshot before the update, and Adam
+// (optim.rs:40-60) with the projection (fit.rs:399-424), for the parameter
+// columns [64 x, 64 x + 64) of block x. Every block sums the loss
+// partials in reduce_partials' order and decides from st[iter & 1], so all
+// take the same decision; block 0 records it in st[(iter + 1) & 1] (and the
+// loss, the loss history and `halt`). An iteration launched after the stop
+// only carries the state forward (its raster kernels returned at entry).
+__global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restrict__ partials,
+                                                           const double* __restrict__ partial_loss, int nblk,
+                                                           int T, double npix3, FitTail ft) {
+    __shared__ float part[RED_WAVES][64];
     __shared__ int decision;
-    if (threadIdx.x == 0) {
-        int d = -1;
-        if (st->stop < 0) {
-            float L = loss[0];
+    const FitState cur = ft.st[ft.iter & 1];
+    FitState* const nxt = ft.st + ((ft.iter + 1) & 1);
+    // The stop is read from the state, not from `halt`, which block 0 of this
+    // kernel may already have set while another block starts.
+    if (cur.stop >= 0) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) *nxt = cur;
+        return;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cols = T * NP;
+    const int col = blockIdx.x * 64 + lane;
+    float acc = 0.0f;
+    if (col < cols) {
+        const float* base = partials + col;
+        int r0 = (nblk * wave) / RED_WAVES, r1 = (nblk * (wave + 1)) / RED_WAVES;
+        int rr = r0;
+        for (; rr + 4 <= r1; rr += 4) {
+            float v0 = base[(size_t)rr * cols], v1 = base[(size_t)(rr + 1) * cols];
+            float v2 = base[(size_t)(rr + 2) * cols], v3 = base[(size_t)(rr + 3) * cols];
+            acc = (((acc + v0) + v1) + v2) + v3;
+        }
+        for (; rr < r1; rr++) acc += base[(size_t)rr * cols];
+    }
+    part[wave][lane] = acc;
+    if (wave == 1) {
+        double s = 0.0;
+        for (int rr = lane; rr < nblk; rr += 64) s += partial_loss[rr];
+        s = wave_sum_f64(s);
+        if (lane == 0) {
+            // fit.rs:243-288
+            const float L = (float)(s / npix3);
+            FitState n = cur;
+            int d = -1;
             if (!isfinite(L)) {
-                st->stop = STOP_DIVERGED;  // before the optimizer sees it (fit.rs:259-265)
+                n.stop = STOP_DIVERGED;
             } else {
-                losses_out[st->n_losses++] = L;
-                bool improved = L + min_delta < st->best_loss;
+                const bool improved = L + ft.min_delta < cur.best_loss;
                 if (improved) {
-                    st->best_loss = L;
-                    st->best_iter = iter;
-                    st->since = 0;
+                    n.best_loss = L;
+                    n.best_iter = ft.iter;
+                    n.since = 0;
                 } else {
-                    st->since += 1;
+                    n.since = cur.since + 1;
                 }
-                bool converged = patience >= 0 && (long long)st->since >= patience;
-                if (converged) st->stop = STOP_CONVERGED;
+                n.n_losses = cur.n_losses + 1;
+                const bool converged = ft.patience >= 0 && (long long)n.since >= ft.patience;
+                if (converged) n.stop = STOP_CONVERGED;
                 d = (improved ? 1 : 0) | (converged ? 2 : 0);
             }
+            decision = d;
+            if (blockIdx.x == 0) {
+                *ft.loss = L;
+                if (d >= 0) ft.losses_out[cur.n_losses] = L;
+                *nxt = n;
+                if (n.stop >= 0) *ft.halt = n.stop;
+            }
         }
-        decision = d;
     }
     __syncthreads();
-    int d = decision;
-    if (d < 0) return;
-    if (d & 1)
-        for (int i = threadIdx.x; i < n; i += blockDim.x) best_params[i] = params[i];
-    if (d & 2) return;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float g = grads[i];
-        float mi = beta1 * m[i] + (1.0f - beta1) * g;
-        float vi = beta2 * v[i] + (1.0f - beta2) * g * g;
-        m[i] = mi;
-        v[i] = vi;
-        float pv = params[i] - lr[i] * (mi / bc1) / (sqrtf(vi / bc2) + eps);
-        int j = i % NP;
-        if (pv != pv) pv = 0.5f;
-        if (j < 6) pv = rust_clamp(pv, -0.25f, 1.25f);
-        else if (j < 9) pv = rust_clamp(pv, 0.0f, 1.0f);
-        else pv = rust_clamp(pv, 1e-3f, 0.999f);
-        params[i] = pv;
+    const int d = decision;
+    if (wave == 0 && col < cols) {
+        float g = part[0][lane];
+        for (int q = 1; q < RED_WAVES; q++) g += part[q][lane];
+        ft.grads[col] = g;
+        if (d >= 0) {
+            if (d & 1) ft.best[col] = ft.params[col];
+            if (!(d & 2)) {
+                const float mi = ft.beta1 * ft.m[col] + (1.0f - ft.beta1) * g;
+                const float vi = ft.beta2 * ft.v[col] + (1.0f - ft.beta2) * g * g;
+                ft.m[col] = mi;
+                ft.v[col] = vi;
+                float pv = ft.params[col] - ft.lr[col] * (mi / ft.bc1) / (sqrtf(vi / ft.bc2) + ft.eps);
+                const int j = col % NP;
+                if (pv != pv) pv = 0.5f;
+                if (j < 6) pv = rust_clamp(pv, -0.25f, 1.25f);
+                else if (j < 9) pv = rust_clamp(pv, 0.0f, 1.0f);
+                else pv = rust_clamp(pv, 1e-3f, 0.999f);
+                ft.params[col] = pv;
+            }
+        }
     }
 }
 
@@ -1921,12 +1961,10 @@ hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const Sr
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_fit_tail(int iter, const float* loss, float* params, const float* grads, float* m, float* v,
-                           const float* lr, int n, float beta1, float beta2, float eps, float bc1, float bc2,
-                           float min_delta, long long patience, FitState* st, float* losses_out,
-                           float* best_params, hipStream_t s) {
-    hipLaunchKernelGGL(fit_tail, dim3(1), dim3(256), 0, s, iter, loss, params, grads, m, v, lr, n, beta1, beta2,
-                       eps, bc1, bc2, min_delta, patience, st, losses_out, best_params);
+hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int T, double npix3,
+                           const FitTail& ft, hipStream_t s) {
+    const dim3 grid((unsigned)((T * NP + 63) / 64));
+    hipLaunchKernelGGL(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, T, npix3, ft);
     return hipGetLastError();
 }
 

@@ -270,15 +270,17 @@ int backward_segments(int T, int cap2, bool det, size_t blocks, int cus);
 // kernels (for comparing the two paths).
 bool fused_gradients(int mode, int nseg, int cap2, int T);
 
+// `tail` (the fit loop, deterministic MODE_LOSS, B = 1): fit_step in place of
+// reduce_partials, the iteration's bookkeeping and Adam in the same kernel.
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
                     uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt = nullptr,
-                    bool timed = true);
+                    bool timed = true, const drh::FitTail* tail = nullptr);
 
 // run_raster_bufs over pooled buffers.
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
                int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
-               hipStream_t s, const int* halt = nullptr);
+               hipStream_t s, const int* halt = nullptr, const drh::FitTail* tail = nullptr);
 
 // Called by drh_create with the context's device current: takes the device
 // address of the scratch array of drh_fused_loss_backward_noalloc on that

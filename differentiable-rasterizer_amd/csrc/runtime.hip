@@ -298,7 +298,8 @@ bool fused_gradients(int mode, int nseg, int cap2, int T) {
 
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
-                    uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt, bool timed) {
+                    uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt, bool timed,
+                    const drh::FitTail* tail) {
     const bool fast = !(flags & DRH_EXACT_MATH);
     const bool det = (flags & DRH_DETERMINISTIC) != 0;
     const dim3 grid = drh::raster_grid(B, W, H);
@@ -356,7 +357,11 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
         KernelTimer kt(ctx, TK_BACKWARD, s, timed);
         HIP_TRY(drh::launch_backward(mode, fast, bufs.cap2 < T, a, s), "backward_kernel launch");
     }
-    if (det) {
+    if (det && tail) {
+        KernelTimer kt(ctx, TK_ADAM, s, timed);
+        HIP_TRY(drh::launch_fit_step(a.partials, a.partial_loss, nblk, T, 3.0 * (double)H * (double)W, *tail, s),
+                "fit_step launch");
+    } else if (det) {
         KernelTimer kt(ctx, TK_REDUCE, s, timed);
         HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3.0 * (double)H * (double)W, out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
@@ -377,7 +382,7 @@ int backward_segments(int T, int cap2, bool det, size_t blocks, int cus) {
 
 int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B, int T,
                int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses, uint32_t flags,
-               hipStream_t s, const int* halt) {
+               hipStream_t s, const int* halt, const drh::FitTail* tail) {
     const bool det = (flags & DRH_DETERMINISTIC) != 0;
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
@@ -434,7 +439,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     bufs.tent = tent.get<drh::TileEnt>();
     bufs.tn = tn.get<int>();
     return run_raster_bufs(ctx, mode, params, bgs, img_in, B, T, H, W, sigma, out_img, out_grads, out_losses, flags,
-                           bufs, s, halt);
+                           bufs, s, halt, true, tail);
 }
 
 }  // namespace drh_rt
