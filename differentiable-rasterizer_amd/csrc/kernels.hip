@@ -107,7 +107,7 @@ static_assert(ORD_MAX_CELLS <= 0xFFFF, "cell indices fit 16 bits");
 __device__ inline float slope(float dx, float dy) { return dy > 0.0f ? __fdividef(dx, dy) : 0.0f; }
 
 __device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sigma, int shift) {
-    Reach r;
+    Reach r{};
     const BlockBox bb = block_box(p, W, H, sigma, shift);  // finite vertices, alpha > 0
     r.lo = 1u | 1u << 16;  // culled
     r.hi = 0u;
