@@ -90,8 +90,14 @@ struct OrderArgs {
     int* perm;
     int gx, gy;
     int shift = 4;
+    // Optional (the tile order, gy ceil(T / 32) <= ORD_ROW_WORDS): the live
+    // triangles whose cull box meets each cell row, in index order:
+    // rows[(b gy + y) T + i] for i < row_n[b gy + y].
+    int* rows = nullptr;
+    int* row_n = nullptr;
 };
 constexpr int ORD_MAX_CELLS = 8192;
+constexpr int ORD_ROW_WORDS = 2048;  // LDS bit-mask words of the row lists (one bit per triangle and row)
 
 struct RasterArgs {
     int B, T, H, W;
@@ -120,6 +126,11 @@ struct RasterArgs {
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
     const int* perm_bwd;   // block order of the backward kernel or null
     int perm_tiles;        // perm_bwd orders 8x8 tiles (one-wave fused kernel), not blocks
+    // OrderArgs::rows / row_n of 8x8-tile rows (row_gy per scene), or null:
+    // the one-wave fused kernel's lists then scan every triangle
+    const int* rows;
+    const int* row_n;
+    int row_gy;
     const int* halt;       // null, or a flag: every block returns at entry once it is >= 0
     // Split backward (nseg > 1, with a block order): in the nsplit heaviest
     // blocks of each scene, segment s of a tile's recorded entries,

@@ -150,13 +150,17 @@ __device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sig
 // cull box alone also counts the cells between a thin or slanted triangle's
 // edges and its box, which are often most of them. r is taken by value: its
 // fields stay in registers over the rows.
-__device__ inline void reach_rows(const Reach r, int W, int H, int shift, int j, int m, int* cells, int pitch) {
+// With `rowmask` it also sets the triangle's bit k in the masks of every row of
+// its cull box (words 32-bit words per row).
+__device__ inline void reach_rows(const Reach r, int W, int H, int shift, int j, int m, int* cells, int pitch,
+                                  uint32_t* rowmask, int words, int k) {
     const float cs = (float)(1 << shift), rH = 1.0f / (float)H, cell_h = cs * rH, wc = (float)W / cs;
     const float band = (cs - 1.0f) * rH + 2.0f * r.far, y_first = 0.5f * rH - r.far;
     const float c0_off = (0.5f - cs) / cs, c1_off = -0.5f / cs;
     auto short_x = [&](float y) { return y <= r.ym ? fmaf(y - r.yt, r.s_tm, r.xt) : fmaf(y - r.ym, r.s_mb, r.xm); };
     const int x0 = r.x0(), x1 = r.x1(), y1 = r.y1();
     for (int y = r.y0() + j; y <= y1; y += m) {
+        if (rowmask) atomicOr(&rowmask[y * words + (k >> 5)], 1u << (k & 31));
         const float ya = fmaf((float)y, cell_h, y_first);
         const float ca = fmaxf(ya, r.yt), cb = fminf(ya + band, r.yb);
         if (!(ca <= cb)) continue;
@@ -307,7 +311,7 @@ __device__ inline void setup_one(const float* __restrict__ params, size_t i, int
 // slot i to rank i / B of scene i % B, so the heaviest blocks of every scene go
 // first. Nothing crosses workgroups: a device-wide hand-off would cost more
 // than the order saves.
-constexpr int SETUP_THREADS = 1024, ORD_BUCKETS = 1024, ORD_REACH = 512;
+constexpr int SETUP_THREADS = 1024, ORD_BUCKETS = 1024, ORD_REACH = 256;
 static_assert(ORD_BUCKETS % SETUP_THREADS == 0 && SETUP_THREADS % 64 == 0, "order workgroup shape");
 
 // Inclusive prefix sum over the wave's lanes (every lane active).
@@ -397,6 +401,11 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
     // are loaded before the work that precedes its Reach (the first batch's
     // before the cells are cleared).
     __shared__ Reach reach[ORD_REACH];
+    __shared__ uint32_t rowmask_s[ORD_ROW_WORDS];
+    const int words = (T + 31) / 32;
+    uint32_t* const rowmask = o.rows && o.gy * words <= ORD_ROW_WORDS ? rowmask_s : nullptr;
+    if (rowmask)
+        for (int c = threadIdx.x; c < o.gy * words; c += SETUP_THREADS) rowmask[c] = 0u;
     float pk[NP];
     auto load_batch = [&](int k0) {
         const int k = k0 + (int)threadIdx.x;
@@ -412,8 +421,26 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
         __syncthreads();
         const int m = min(SETUP_THREADS / nt, 16);
         for (int w = threadIdx.x; w < nt * m; w += SETUP_THREADS)
-            reach_rows(reach[w / m], W, H, o.shift, w % m, m, cells, pitch);
+            reach_rows(reach[w / m], W, H, o.shift, w % m, m, cells, pitch, rowmask, words, k0 + w / m);
         __syncthreads();
+    }
+    if (rowmask) {
+        // each row's set bits in index order, one wave per row: a wave scan of
+        // the words' bit counts places each word's indices
+        const int lane = threadIdx.x & 63;
+        for (int y = threadIdx.x >> 6; y < o.gy; y += SETUP_THREADS / 64) {
+            int* out = o.rows + ((size_t)b * o.gy + y) * T;
+            int carry = 0;
+            for (int w0 = 0; w0 < words; w0 += 64) {
+                const int w = w0 + lane;
+                uint32_t bits = w < words ? rowmask[y * words + w] : 0u;
+                const int cnt = __popc(bits), incl = wave_scan_incl(cnt, lane);
+                int pos = carry + incl - cnt;
+                for (; bits; bits &= bits - 1) out[pos++] = 32 * w + __ffs((int)bits) - 1;
+                carry += __shfl(incl, 63, 64);
+            }
+            if (lane == 0) o.row_n[(size_t)b * o.gy + y] = carry;
+        }
     }
     order_scene(o, cells, b, T);
 }
@@ -692,20 +719,29 @@ enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 // classification then also loads every field any of its branches reads up
 // front (one round trip instead of one per branch level; the other callers
 // keep the lazy loads, whose registers their occupancy needs).
+//
+// With `ilist` (merged lists only) [k0, k1) are positions in ilist, a list of
+// triangle indices in order, and entries hold the triangles' indices instead
+// of their offsets from k0.
 template <bool MERGE = false>
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
-                                 uint32_t* list, int lane, int live, int* kend = nullptr) {
+                                 uint32_t* list, int lane, int live, int* kend = nullptr,
+                                 const int* __restrict__ ilist = nullptr) {
     static_assert(CH >= 128, "a merged list holds two passes of candidates");
     static_assert(R_FLAGS == R_BOX + 4, "the box tests read x0 y0 x1 y1 flags as five consecutive ints");
+    const int kbase = ilist ? 0 : k0;
     int nc = 0;
     if (MERGE) *kend = k1;
     for (int base2 = k0; base2 < k1; base2 += 128) {
         int bf[2][5];  // x0 y0 x1 y1 flags of the triangle k of each pass
+        int kk[2];     // its index
         for (int h = 0; h < 2; h++) {
             // Lanes past the chunk read its last record (in bounds) and are
             // masked out.
-            const int* ri = reinterpret_cast<const int*>(rec + (size_t)min(base2 + 64 * h + lane, k1 - 1) * REC);
+            const int pos = min(base2 + 64 * h + lane, k1 - 1);
+            kk[h] = ilist ? ilist[pos] : pos;
+            const int* ri = reinterpret_cast<const int*>(rec + (size_t)kk[h] * REC);
             for (int f = 0; f < 5; f++) bf[h][f] = ri[R_BOX + f];
         }
         for (int h = 0; h < 2; h++) {
@@ -721,7 +757,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
         if (cand) {
             const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = ((uint32_t)(k - k0) << 1) | (in_box ? 1u : 0u);
+            list[pos] = ((uint32_t)(kk[h] - kbase) << 1) | (in_box ? 1u : 0u);
         }
         nc += (int)__popcll(mask);
         if (MERGE && nc > 64) {
@@ -740,7 +776,7 @@ classify:
         if (c0 + lane < nc) {
             const uint32_t cd = list[c0 + lane];
             kl = cd >> 1;
-            const float* r = rec + (size_t)(k0 + (int)kl) * REC;
+            const float* r = rec + (size_t)(kbase + (int)kl) * REC;
             const int flags = reinterpret_cast<const int*>(r)[R_FLAGS];
             // With MERGE the classification's fields, [R_N, R_EB), are loaded
             // together: the empty asm uses them all here, so that the compiler
@@ -1057,7 +1093,7 @@ __device__ inline TileGeo tile_geo_split(int W, int H, int gx, int gy, const int
 // split backward's checkpoints too. lw: the wave's LDS list. MERGE: lists of
 // merged chunks (build_list), for a caller that takes every triangle index from
 // the recorded entries; rec_chunks is then meaningless.
-template <int MODE, bool FAST, bool CKPT, bool MERGE = false>
+template <int MODE, bool FAST, bool CKPT, bool MERGE = false, bool ROWS = false>
 __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* __restrict__ rec, const TileGeo& tg,
                                               uint64_t validm, float rsig, float sig, uint32_t* lw,
                                               float (&col)[3], Trans& tot, int& n2, int& rec_chunks) {
@@ -1078,18 +1114,28 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
     float* ckw = nck > 0 ? a.ckpt + (size_t)uniform_u32((uint32_t)tg.tile) * nck * (CKPT_WORDS * 64) : nullptr;
 
     static_assert(!(MERGE && CKPT), "checkpoints count entries per chunk");
+    static_assert(MERGE || !ROWS, "row lists are merged lists");
+    // ROWS: merged lists over the tile row's triangles, which setup_records listed
+    const int* ilist = nullptr;
+    int nlist = T;
+    if (ROWS) {
+        const size_t row = (size_t)tg.b * a.row_gy + (tg.ty0 >> 3);
+        ilist = a.rows + row * T;
+        nlist = a.row_n[row];
+    }
     int k1 = 0;
-    for (int c = 0; MERGE ? k1 < T : c < n_chunks; c++) {
+    for (int c = 0; MERGE ? k1 < nlist : c < n_chunks; c++) {
         const int k0 = MERGE ? k1 : c * CH;
-        k1 = MERGE ? T : min(T, k0 + CH);
+        k1 = MERGE ? nlist : min(T, k0 + CH);
         int count = tg.live ? build_list<MERGE>(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
-                                                tg.cx1, tg.cy1, lw, lane, F_LIVE, &k1)
+                                                tg.cx1, tg.cy1, lw, lane, F_LIVE, &k1, ilist)
                             : 0;
+        const int kbase = ilist ? 0 : k0;
         uint32_t nxt = lw[0];  // the next entry is read one iteration ahead
         for (int i = 0; i < count; i++) {
             const uint32_t ent = uniform_u32(nxt);
             nxt = lw[min(i + 1, CH - 1)];
-            const int k = k0 + (int)(ent >> 8);
+            const int k = kbase + (int)(ent >> 8);
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
             float w = 0.0f, cov;
@@ -1632,8 +1678,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
 // order, of tiles (perm_tiles) or of blocks four tiles at a time
 // (tile_geo_wave). Its loss partials are per tile, summed
 // per block in wave order by sum_losses, as the four-wave blocks sum them.
-// Used where fused_kernel would be, outside the deterministic mode.
-template <int MODE, bool FAST>
+// Used where fused_kernel would be, outside the deterministic mode. ROWS: its
+// lists scan the tile row's triangles (RasterArgs::rows), else all of them.
+template <int MODE, bool FAST, bool ROWS>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fused_tile_kernel(RasterArgs a, const float* __restrict__ records,
                                                                                 const TileEnt* __restrict__ ents) {
     static_assert(MODE == MODE_LOSS || MODE == MODE_GRAD_IN, "gradient modes only");
@@ -1654,7 +1701,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     Trans tot = {1.0f, 0, 0};
     int n2, rec_chunks;
     // merged chunks: the sweep below reads each entry's triangle index
-    forward_sweep<MODE, FAST, false, true>(a, rec, tg, validm, rsig, sig, list, col, tot, n2, rec_chunks);
+    forward_sweep<MODE, FAST, false, true, ROWS>(a, rec, tg, validm, rsig, sig, list, col, tot, n2, rec_chunks);
     if (MODE == MODE_LOSS && a.out_img && tg.valid)
         for (int ch = 0; ch < 3; ch++) a.out_img[img_index(a, tg.pix, b, ch)] = col[ch];
     for (int ch = 0; ch < 3; ch++) st.g0[ch] = 0.0f;
@@ -2057,10 +2104,15 @@ static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_
         return;
     }
     const dim3 tiles(grid.x * grid.y * grid.z * WAVES);
-    if (fast)
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+    const bool rows = a.rows && a.row_n;
+    if (fast && rows)
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+    else if (fast)
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, true, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+    else if (rows)
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, false, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
     else
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        hipLaunchKernelGGL((fused_tile_kernel<MODE, false, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
 }
 
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {

@@ -56,6 +56,7 @@ enum Kind : uint64_t {
     K_RESIZE_TAB,
     K_RESIZE_TMP,
     K_CKPT,
+    K_ROWS,
 };
 
 // Bytes the pool keeps at least (crates/diffrast-gpu/src/lib.rs:123-130);
@@ -239,7 +240,16 @@ struct RasterBufs {
     int nseg = 1, seg_m = 0, nsplit = 0;  // its segments, entries per segment, split blocks per scene
     bool fused = false;             // one fused kernel (fused_gradients); pq, pg0, pze, tn unused
     bool order_tiles = false;       // `order` ranks 8x8 tiles (one-wave fused kernel only), not blocks
+    int* rows = nullptr;            // with order_tiles: B*2gy*T triangle indices per 8x8-tile row, or null
+    int* row_n = nullptr;           // B*2gy counts
 };
+
+// The one-wave fused kernel's lists scan the triangles of their tile row
+// (OrderArgs::rows) from this many triangles on. Below it a tile's box tests
+// are at most a few passes of 64 and making the row lists costs setup_records
+// more than it saves (measured at T = 128: +3.3 us of setup, the fused kernel
+// unchanged; at T = 512 with small triangles the fused kernel 35.7 -> 31.7 us).
+constexpr int ROW_LISTS_MIN_T = 256;
 
 // Split of the backward's sweep over a tile's recorded entries. A tile's sweep
 // is sequential, and the tiles with the longest lists sit together (a block's

@@ -306,7 +306,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     const int nblk = (int)(grid.x * grid.y);
     drh::OrderArgs ord{};
     if (bufs.order)
-        ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3}
+        ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3, bufs.rows, bufs.row_n}
                                : drh::OrderArgs{bufs.order, (int)grid.x, (int)grid.y, 4};
     {
         KernelTimer kt(ctx, TK_SETUP, s, timed);
@@ -338,6 +338,9 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
     a.perm_bwd = ord.perm;
     a.perm_tiles = bufs.order_tiles ? 1 : 0;
+    a.rows = bufs.order_tiles ? bufs.rows : nullptr;
+    a.row_n = bufs.order_tiles ? bufs.row_n : nullptr;
+    a.row_gy = 2 * (int)grid.y;
     a.halt = halt;
     a.nseg = bufs.ckpt && ord.perm ? bufs.nseg : 1;
     a.seg_m = bufs.seg_m;
@@ -387,7 +390,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
     const size_t ntiles = (size_t)B * nblk * drh::WAVES;
-    Lease rec, partials, ploss, pq, pg0, pze, tent, tn, order, ckpt;
+    Lease rec, partials, ploss, pq, pg0, pze, tent, tn, order, ckpt, rows;
     RasterBufs bufs;
     // whole 64-byte lines per tile (8 entries), as the fused kernel needs
     bufs.cap2 = tile_entries(ntiles, (T + 7) & ~7);
@@ -414,6 +417,14 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         const size_t cells = (size_t)B * nblk * (bufs.order_tiles ? drh::WAVES : 1);
         if ((rc = order.acquire(ctx, K_ORDER, cells * sizeof(int), s))) return rc;
         bufs.order = order.get<int>();
+        // the tile rows' triangle lists, where their bit masks fit setup_records' LDS
+        const size_t trows = (size_t)B * 2 * grid.y;
+        if (bufs.order_tiles && T >= ROW_LISTS_MIN_T &&
+            (size_t)2 * grid.y * ((T + 31) / 32) <= (size_t)drh::ORD_ROW_WORDS) {
+            if ((rc = rows.acquire(ctx, K_ROWS, (trows * T + trows) * sizeof(int), s))) return rc;
+            bufs.rows = rows.get<int>();
+            bufs.row_n = bufs.rows + trows * T;
+        }
     }
     if (mode != drh::MODE_RENDER) {
         if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))

@@ -10,8 +10,10 @@ gradient norm), and, with DRH_DETERMINISTIC, be bit-identical from call to call.
 cases are sized to take the ordered paths: 4 scenes of 160 x 200 px are 4 x 10 x 13 =
 520 blocks; 2 scenes of 720 x 768 px have 90 x 96 tiles each, past the tile order's
 8192 cells, so their one-wave fused kernel takes the block order; 2 scenes of 1100
-small triangles take the order workgroup's triangles in three batches of up to 512
-and the records in two workgroups of 1024.
+small triangles take the order workgroup's triangles in five batches of up to 256
+and the records in two workgroups of 1024. From 256 triangles on, the one-wave
+fused kernel's lists scan only the triangles of their tile row, which setup_records
+lists (the small-triangle cases, and 300 large triangles at 256 x 256).
 """
 
 import numpy as np
@@ -48,11 +50,12 @@ def scenes(kind, B, T, seed):
 
 # (kind, B, H, W, T, sigma): forward and backward ordered; backward only (T > 256)
 CASES = [("uniform", 4, 160, 200, 100, 0.002), ("small", 3, 200, 208, 300, 0.003),
-         ("uniform", 2, 720, 768, 40, 0.002), ("small", 2, 256, 256, 1100, 0.002)]
+         ("uniform", 2, 720, 768, 40, 0.002), ("small", 2, 256, 256, 1100, 0.002),
+         ("uniform", 2, 256, 256, 300, 0.002)]
 
 
 @pytest.mark.parametrize("kind,B,H,W,T,sigma", CASES,
-                         ids=["ordered", "backward-ordered", "large-block-order", "many-triangles"])
+                         ids=["ordered", "backward-ordered", "large-block-order", "many-triangles", "row-lists-large"])
 def test_ordered_render_fused_and_from_grad_match_oracle(ctx, orc, kind, B, H, W, T, sigma):
     assert B * -(-H // 16) * -(-W // 16) > 256  # more blocks than CUs: the order is made
     params, bgs = scenes(kind, B, T, 50)
