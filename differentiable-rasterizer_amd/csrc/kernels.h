@@ -95,6 +95,10 @@ struct OrderArgs {
     // rows[(b gy + y) T + i] for i < row_n[b gy + y].
     int* rows = nullptr;
     int* row_n = nullptr;
+    // Scalings of the reach estimate, set by launch_setup from W, H and shift:
+    // 1/H, a cell's height 2^shift / H, W / 2^shift, and the offsets of the
+    // cell-index bounds (0.5 - 2^shift) / 2^shift and -0.5 / 2^shift.
+    float r_h = 0, cell_h = 0, w_cells = 0, c0_off = 0, c1_off = 0;
 };
 constexpr int ORD_MAX_CELLS = 8192;
 constexpr int ORD_ROW_WORDS = 2048;  // LDS bit-mask words of the row lists (one bit per triangle and row)

@@ -152,11 +152,11 @@ __device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sig
 // fields stay in registers over the rows.
 // With `rowmask` it also sets the triangle's bit k in the masks of every row of
 // its cull box (words 32-bit words per row).
-__device__ inline void reach_rows(const Reach r, int W, int H, int shift, int j, int m, int* cells, int pitch,
+__device__ inline void reach_rows(const Reach r, const OrderArgs& o, int j, int m, int* cells, int pitch,
                                   uint32_t* rowmask, int words, int k) {
-    const float cs = (float)(1 << shift), rH = 1.0f / (float)H, cell_h = cs * rH, wc = (float)W / cs;
+    const float cs = (float)(1 << o.shift), rH = o.r_h, cell_h = o.cell_h, wc = o.w_cells;
     const float band = (cs - 1.0f) * rH + 2.0f * r.far, y_first = 0.5f * rH - r.far;
-    const float c0_off = (0.5f - cs) / cs, c1_off = -0.5f / cs;
+    const float c0_off = o.c0_off, c1_off = o.c1_off;
     auto short_x = [&](float y) { return y <= r.ym ? fmaf(y - r.yt, r.s_tm, r.xt) : fmaf(y - r.ym, r.s_mb, r.xm); };
     const int x0 = r.x0(), x1 = r.x1(), y1 = r.y1();
     for (int y = r.y0() + j; y <= y1; y += m) {
@@ -419,9 +419,10 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
         if ((int)threadIdx.x < nt) reach[threadIdx.x] = make_reach(pk, W, H, sigma, o.shift);
         load_batch(k0 + ORD_REACH);
         __syncthreads();
-        const int m = min(SETUP_THREADS / nt, 16);
+        // a power of two, so that the thread's triangle and row are a shift and a mask
+        const int lg = 31 - __clz(min(SETUP_THREADS / nt, 16)), m = 1 << lg;
         for (int w = threadIdx.x; w < nt * m; w += SETUP_THREADS)
-            reach_rows(reach[w / m], W, H, o.shift, w % m, m, cells, pitch, rowmask, words, k0 + w / m);
+            reach_rows(reach[w >> lg], o, w & (m - 1), m, cells, pitch, rowmask, words, k0 + (w >> lg));
         __syncthreads();
     }
     if (rowmask) {
@@ -2024,8 +2025,15 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     // with one, a last workgroup per scene makes it
     const int n = o.perm ? SETUP_THREADS : 64;
     const int gx = (T + n - 1) / n + (o.perm || T == 0 ? 1 : 0);
+    OrderArgs oa = o;
+    const float cs = (float)(1 << o.shift);
+    oa.r_h = 1.0f / (float)H;
+    oa.cell_h = cs * oa.r_h;
+    oa.w_cells = (float)W / cs;
+    oa.c0_off = (0.5f - cs) / cs;
+    oa.c1_off = -0.5f / cs;
     hipLaunchKernelGGL(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
-                       zero_grads, bg_src, bg_dst, o, halt, head, head_val);
+                       zero_grads, bg_src, bg_dst, oa, halt, head, head_val);
     return hipGetLastError();
 }
 
