@@ -80,6 +80,21 @@ def test_patience_stops_with_a_last_step(ctx):  # fit.rs:277-281, 530-540
     f.close()
 
 
+def test_patience_zero_stops_after_the_first_snapshot(ctx, orc):  # fit.rs:267-281
+    # patience 0: the first iteration improves on an infinite best loss and, with
+    # since = 0 >= 0, converges: the best scene is the initial one (snapshotted
+    # before the update, in every block of parameter columns) and no update runs
+    target = synth.blob_target(5, 24, 24)
+    init, bg = synth.seed_scene(target, 30, 5)  # 300 parameters: several blocks of 64 columns
+    r = ctx.fit(target, init, bg, iters=20, patience=0)
+    c = orc.fit(target, init, bg, iters=20, patience=0)
+    assert r["stop_reason"] == c["stop_reason"] == "Converged"
+    assert len(r["losses"]) == len(c["losses"]) == 1 and r["best_iter"] == c["best_iter"] == 0
+    assert np.array_equal(r["best_params"].reshape(-1), np.asarray(init, np.float32).reshape(-1))
+    assert np.array_equal(r["params"].reshape(-1), np.asarray(init, np.float32).reshape(-1))
+    assert abs(r["losses"][0] - c["losses"][0]) <= 1e-4 * abs(c["losses"][0])
+
+
 def test_divergence_returns_none_before_recording(ctx):  # fit.rs:259-265
     bad = np.full((16, 16, 3), 0.4, np.float32)
     bad[3, 4, 1] = float("nan")
