@@ -682,8 +682,31 @@ __device__ inline void lds_add(lds_float* p, float v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
+// Sum over the wave (every lane active) by the butterfly v += v[lane ^ off]
+// for off = 32, 16, ..., 1, so every lane ends with the same, fixed-order sum.
+// The exchanges within 32 lanes are ds_swizzle (xor 16, 8, 4) and DPP quad
+// permutes (xor 2, 1) on the two halves of the double, which skip the
+// address computation and LDS round trip of a bpermute; xor 32 stays a
+// bpermute.
+template <int pattern>
+__device__ inline double swizzle_f64(double v) {
+    const int lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)__double_as_longlong(v), pattern);
+    const int hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(__double_as_longlong(v) >> 32), pattern);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+template <int ctrl>
+__device__ inline double dpp_f64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)__double_as_longlong(v), ctrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(__double_as_longlong(v) >> 32), ctrl, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
 __device__ inline double wave_sum_f64(double v) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += __shfl_xor(v, 32, 64);
+    v += swizzle_f64<(16 << 10) | 0x1F>(v);  // bit mode: and 0x1F, or 0, xor 16
+    v += swizzle_f64<(8 << 10) | 0x1F>(v);
+    v += swizzle_f64<(4 << 10) | 0x1F>(v);
+    v += dpp_f64<DPP_XOR2>(v);
+    v += dpp_f64<DPP_XOR1>(v);
     return v;
 }
 
