@@ -480,8 +480,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(scenes are independent; see DESIGN.md for how batches would shard)", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path "
+              "(scenes are independent: each GPU would take a slice of the batch)", file=sys.stderr)
         sys.exit(2)
 
     import torch

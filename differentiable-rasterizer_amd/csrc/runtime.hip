@@ -629,7 +629,7 @@ int drh_create(drh_ctx** out) {
     *out = nullptr;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
-        return fail(DRH_ERR_NO_DEVICE, "no HIP device found; this build has no CPU path");
+        return fail(DRH_ERR_NO_DEVICE, "no HIP device found; there is no CPU path");
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
     hipDeviceProp_t prop;

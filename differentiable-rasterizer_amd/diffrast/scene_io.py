@@ -274,7 +274,7 @@ def encode_srgb(images):
     copied through and returned as a numpy uint8 array of the same shape."""
     try:
         import torch
-    except ImportError:  # pragma: no cover - torch is part of this build
+    except ImportError:  # pragma: no cover - torch is a dependency of the package
         torch = None
     if torch is not None and isinstance(images, torch.Tensor) and images.is_cuda:
         from . import torch_layer

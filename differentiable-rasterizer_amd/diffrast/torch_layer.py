@@ -49,7 +49,7 @@ def _parse_device(name: str) -> None:
         return
     if name == "cpu":
         raise ValueError(
-            'device="cpu" is not available: this build runs only on the GPU '
+            'device="cpu" is not available: the rasterizer runs only on the GPU '
             '(use "gpu" or "auto")')
     raise ValueError(f'unknown device {name!r} — expected "cpu", "gpu" or "auto"')
 
@@ -61,7 +61,7 @@ def _check_sigma(sigma: float) -> None:
 
 def _gpu() -> torch.device:
     if not torch.cuda.is_available():
-        raise RuntimeError("no HIP device is visible; this build has no CPU path")
+        raise RuntimeError("no HIP device is visible; there is no CPU path")
     return torch.device("cuda", torch.cuda.current_device())
 
 

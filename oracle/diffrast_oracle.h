@@ -4,8 +4,8 @@
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
  * CPU implementation (crates/diffrast/src/{raster,grad,canvas,optim,fit}.rs),
  * used by tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py
- * as the checker. The product (libdiffrast_hip.so and the Python package) never
- * links, loads or calls it.
+ * to check the GPU results against. The product (libdiffrast_hip.so and the
+ * Python package) never links, loads or calls it.
  *
  * Layouts follow the reference exactly:
  *   params  : T x 10 floats per scene, [x0,y0,x1,y1,x2,y2,r,g,b,a]

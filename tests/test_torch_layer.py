@@ -1,6 +1,6 @@
 """The torch drop-in, after the reference's python/test_torch_layer.py.
 
-Same cases and bars. Two deliberate differences, both from this build having
+Same cases and bars. Two deliberate differences, both from the package having
 no CPU backend (the product never runs the oracle): `device="cpu"` raises
 ValueError instead of running a CPU path, and "the GPU agrees with the CPU
 but is not bit-identical" compares the HIP path with the oracle.
@@ -126,7 +126,7 @@ def test_rasterize_routes_to_the_gpu(orc):  # test_torch_layer.py:126-144
 
 
 def test_cpu_device_is_rejected():
-    # No CPU backend in this build: "cpu" fails loudly rather than silently
+    # No CPU backend: "cpu" fails loudly rather than silently
     # running something else (the reference runs its Rust CPU path).
     p = random_params(1, 4, generator=_gen(0))
     with pytest.raises(ValueError):
