@@ -1026,11 +1026,23 @@ __device__ inline TileGeo tile_at(int W, int H, int gx, int gy, int b, int bx, i
     // raster.rs:138-140 pixel centre, correctly rounded division.
     t.p.px = ((float)t.x + 0.5f) / (float)W;
     t.p.py = ((float)t.y + 0.5f) / (float)H;
-    // Corners of the tile's pixel-centre rectangle, for the list classification.
-    t.cx0 = ((float)t.tx0 + 0.5f) / (float)W;
-    t.cy0 = ((float)t.ty0 + 0.5f) / (float)H;
-    t.cx1 = ((float)(t.tx1 - 1) + 0.5f) / (float)W;
-    t.cy1 = ((float)(t.ty1 - 1) + 0.5f) / (float)H;
+    // Corners of the tile's pixel-centre rectangle, for the list classification:
+    // the centres of the lanes at pixels (tx0, ty0) and (tx1 - 1, ty1 - 1), read
+    // across the wave (every lane is active here) instead of divided again. A
+    // tile that is not live reads in-range lanes and never uses them. The
+    // moves keep the corners in VGPRs: as scalar operands the classification's
+    // FMAs with them would issue at the slower rate.
+    const int lx = min(max(t.tx1 - 1 - t.tx0, 0), TILE - 1), ly = min(max(t.ty1 - 1 - t.ty0, 0), TILE - 1);
+    auto lane_value = [](float v, int l) {
+        const int s = __builtin_amdgcn_readlane(__float_as_int(v), l);
+        int r;
+        asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(s));
+        return __int_as_float(r);
+    };
+    t.cx0 = lane_value(t.p.px, 0);
+    t.cy0 = lane_value(t.p.py, 0);
+    t.cx1 = lane_value(t.p.px, lx);
+    t.cy1 = lane_value(t.p.py, ly * TILE);
     t.pix = ((size_t)t.b * H + (t.valid ? t.y : 0)) * W + (t.valid ? t.x : 0);
     t.tile = (((size_t)t.b * gy + t.by) * gx + t.bx) * WAVES + t.wave;
     return t;
