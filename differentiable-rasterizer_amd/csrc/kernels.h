@@ -221,7 +221,7 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
 // its per-block sums.
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s);
 // per: loss partials per block (1, or WAVES for the fused kernel's per-tile partials outside the
-// deterministic mode).
+// deterministic mode; hipErrorInvalidValue otherwise, or for nblk < 1).
 hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int per, double npix3, float* losses,
                              hipStream_t s, const int* halt = nullptr);
 // Loss partials per block that a gradient call's raster kernels write.

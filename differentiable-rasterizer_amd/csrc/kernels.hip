@@ -1800,28 +1800,65 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
         sweep(std::false_type{});
 }
 
+// Lane `lane`'s share of a scene's block loss sums: blocks lane, lane + 64, ...
+// added in turn to a double, each block's PER partials summed in order first.
+// The loads of SUM_UNROLL blocks are issued before any of them is added, so up
+// to 64 SUM_UNROLL blocks take one round of loads.
+constexpr int SUM_UNROLL = 8;
+template <int PER>
+__device__ inline double lane_block_losses(const double* __restrict__ pl, int nblk, int lane) {
+    double l = 0.0;
+    for (int r0 = lane; r0 < nblk; r0 += 64 * SUM_UNROLL) {
+        double part[SUM_UNROLL][PER];
+#pragma unroll
+        for (int u = 0; u < SUM_UNROLL; u++) {
+            const int r = min(r0 + 64 * u, nblk - 1);
+#pragma unroll
+            for (int q = 0; q < PER; q++) part[u][q] = pl[(size_t)r * PER + q];
+        }
+#pragma unroll
+        for (int u = 0; u < SUM_UNROLL; u++) {
+            double lb = part[u][0];
+#pragma unroll
+            for (int q = 1; q < PER; q++) lb += part[u][q];
+            // A select, not a branch, so that every load above is issued first.
+            l = r0 + 64 * u < nblk ? l + lb : l;
+        }
+    }
+    return l;
+}
+
+// base[r * stride] for r in [r0, r1) added in order to 0, ROW_BATCH loads
+// issued before they are added.
+constexpr int ROW_BATCH = 8;
+__device__ inline float sum_rows_in_order(const float* __restrict__ base, size_t stride, int r0, int r1) {
+    float acc = 0.0f;
+    for (int rr = r0; rr < r1; rr += ROW_BATCH) {
+        float v[ROW_BATCH];
+#pragma unroll
+        for (int u = 0; u < ROW_BATCH; u++) v[u] = base[(size_t)min(rr + u, r1 - 1) * stride];
+#pragma unroll
+        for (int u = 0; u < ROW_BATCH; u++) acc = rr + u < r1 ? acc + v[u] : acc;
+    }
+    return acc;
+}
+
 // The per-item loss (canvas.rs:45-58) from the fused kernel's per-block sums,
-// one wave per scene, in the order of backward_kernel's sum.
-// per: partials per block, 1 or WAVES (per tile, summed in wave order first).
-__global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ partial_loss, int nblk, int per,
-                                                 double npix3, float* __restrict__ losses,
-                                                 const int* __restrict__ halt) {
+// one wave per scene, in the order of backward_kernel's sum (the lanes' shares,
+// then the lanes summed).
+// PER: partials per block, 1 or WAVES (per tile, summed in wave order first).
+template <int PER>
+__global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ partial_loss, int nblk, double npix3,
+                                                 float* __restrict__ losses, const int* __restrict__ halt) {
     if (halt && *halt >= 0) return;
     const int b = (int)blockIdx.x, lane = (int)threadIdx.x;
-    const double* pl = partial_loss + (size_t)b * nblk * per;
-    double l = 0.0;
-    for (int r = lane; r < nblk; r += 64) {
-        double lb = pl[(size_t)r * per];
-        for (int q = 1; q < per; q++) lb += pl[(size_t)r * per + q];
-        l += lb;
-    }
-    l = wave_sum_f64(l);
+    const double l = wave_sum_f64(lane_block_losses<PER>(partial_loss + (size_t)b * nblk * PER, nblk, lane));
     if (lane == 0) losses[b] = (float)(l / npix3);
 }
 
 // Sum the per-block partial rows of each scene in block order. One block per
-// (scene, 64 columns); its 16 waves each sum a contiguous range of rows (loads
-// unrolled four deep), and the ranges are combined in row order.
+// (scene, 64 columns); its 16 waves each sum a contiguous range of rows
+// (sum_rows_in_order), and the ranges are combined in row order.
 constexpr int RED_WAVES = 16;
 __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* __restrict__ partials,
                                                                   const double* __restrict__ partial_loss,
@@ -1836,17 +1873,9 @@ __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* _
     const int cols = T * NP;
     const int col = blockIdx.x * 64 + lane;
     float acc = 0.0f;
-    if (col < cols) {
-        const float* base = partials + (size_t)b * nblk * cols + col;
-        int r0 = (nblk * wave) / RED_WAVES, r1 = (nblk * (wave + 1)) / RED_WAVES;
-        int rr = r0;
-        for (; rr + 4 <= r1; rr += 4) {
-            float v0 = base[(size_t)rr * cols], v1 = base[(size_t)(rr + 1) * cols];
-            float v2 = base[(size_t)(rr + 2) * cols], v3 = base[(size_t)(rr + 3) * cols];
-            acc = (((acc + v0) + v1) + v2) + v3;
-        }
-        for (; rr < r1; rr++) acc += base[(size_t)rr * cols];
-    }
+    if (col < cols)
+        acc = sum_rows_in_order(partials + (size_t)b * nblk * cols + col, cols, (nblk * wave) / RED_WAVES,
+                                (nblk * (wave + 1)) / RED_WAVES);
     part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && col < cols) {
@@ -1855,9 +1884,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* _
         grads[(size_t)b * cols + col] = v;
     }
     if (losses && blockIdx.x == 0 && wave == 0) {
-        double s = 0.0;
-        for (int rr = lane; rr < nblk; rr += 64) s += partial_loss[(size_t)b * nblk + rr];
-        s = wave_sum_f64(s);
+        const double s = wave_sum_f64(lane_block_losses<1>(partial_loss + (size_t)b * nblk, nblk, lane));
         if (lane == 0) losses[b] = (float)(s / npix3);
     }
 }
@@ -1913,23 +1940,21 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = T * NP;
     const int col = blockIdx.x * 64 + lane;
-    float acc = 0.0f;
-    if (col < cols) {
-        const float* base = partials + col;
-        int r0 = (nblk * wave) / RED_WAVES, r1 = (nblk * (wave + 1)) / RED_WAVES;
-        int rr = r0;
-        for (; rr + 4 <= r1; rr += 4) {
-            float v0 = base[(size_t)rr * cols], v1 = base[(size_t)(rr + 1) * cols];
-            float v2 = base[(size_t)(rr + 2) * cols], v3 = base[(size_t)(rr + 3) * cols];
-            acc = (((acc + v0) + v1) + v2) + v3;
-        }
-        for (; rr < r1; rr++) acc += base[(size_t)rr * cols];
+    // Wave 0's Adam operands, loaded here so that they arrive with the sums
+    // (only this thread writes column col in this kernel).
+    float p0 = 0.0f, m0 = 0.0f, v0 = 0.0f, lr0 = 0.0f;
+    if (wave == 0 && col < cols) {
+        p0 = ft.params[col];
+        m0 = ft.m[col];
+        v0 = ft.v[col];
+        lr0 = ft.lr[col];
     }
+    float acc = 0.0f;
+    if (col < cols)
+        acc = sum_rows_in_order(partials + col, cols, (nblk * wave) / RED_WAVES, (nblk * (wave + 1)) / RED_WAVES);
     part[wave][lane] = acc;
     if (wave == 1) {
-        double s = 0.0;
-        for (int rr = lane; rr < nblk; rr += 64) s += partial_loss[rr];
-        s = wave_sum_f64(s);
+        const double s = wave_sum_f64(lane_block_losses<1>(partial_loss, nblk, lane));
         if (lane == 0) {
             // fit.rs:243-288
             const float L = (float)(s / npix3);
@@ -1967,13 +1992,13 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
         for (int q = 1; q < RED_WAVES; q++) g += part[q][lane];
         ft.grads[col] = g;
         if (d >= 0) {
-            if (d & 1) ft.best[col] = ft.params[col];
+            if (d & 1) ft.best[col] = p0;
             if (!(d & 2)) {
-                const float mi = ft.beta1 * ft.m[col] + (1.0f - ft.beta1) * g;
-                const float vi = ft.beta2 * ft.v[col] + (1.0f - ft.beta2) * g * g;
+                const float mi = ft.beta1 * m0 + (1.0f - ft.beta1) * g;
+                const float vi = ft.beta2 * v0 + (1.0f - ft.beta2) * g * g;
                 ft.m[col] = mi;
                 ft.v[col] = vi;
-                float pv = ft.params[col] - ft.lr[col] * (mi / ft.bc1) / (sqrtf(vi / ft.bc2) + ft.eps);
+                float pv = p0 - lr0 * (mi / ft.bc1) / (sqrtf(vi / ft.bc2) + ft.eps);
                 const int j = col % NP;
                 if (pv != pv) pv = 0.5f;
                 if (j < 6) pv = rust_clamp(pv, -0.25f, 1.25f);
@@ -2173,7 +2198,13 @@ hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s)
 hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int per, double npix3, float* losses,
                              hipStream_t s, const int* halt) {
     if (B == 0) return hipSuccess;
-    hipLaunchKernelGGL(sum_losses, dim3(B), dim3(64), 0, s, partial_loss, nblk, per, npix3, losses, halt);
+    if (nblk <= 0) return hipErrorInvalidValue;
+    if (per == WAVES)
+        hipLaunchKernelGGL(sum_losses<WAVES>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+    else if (per == 1)
+        hipLaunchKernelGGL(sum_losses<1>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
