@@ -469,3 +469,47 @@ def test_channels_first_layout_gives_the_same_numbers(ctx):
     torch.cuda.synchronize()
     for a, b in zip(out["hwc"], out["chw"]):
         assert torch.equal(a, b)
+
+
+def random_case(i):
+    """Seeded shape i of the sweep: B in [1, 4], H and W in [1, 300], T in [1, 1200]
+    (cut so that the oracle sees at most 1.5e7 pixel-triangle pairs), sigma
+    log-uniform in [1e-4, 0.05], one of the three scene kinds."""
+    rng = np.random.default_rng(7000 + i)
+    B = int(rng.integers(1, 5))
+    H, W = (int(v) for v in rng.integers(1, 301, size=2))
+    T = int(rng.integers(1, 1201))
+    T = max(1, min(T, 15_000_000 // (B * H * W)))
+    sigma = float(10.0 ** rng.uniform(-4.0, np.log10(0.05)))
+    kind = ("uniform", "small", "random")[int(rng.integers(0, 3))]
+    return B, H, W, T, sigma, kind
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_shapes_match_oracle(ctx, orc, i, monkeypatch):
+    # Every gradient path on a seeded random shape: the fast and exact fused
+    # calls, the fixed-order sums and the two-kernel path (DRH_UNFUSED=1: the
+    # split backward and the rebuild past the recorded entries where they
+    # apply) against the oracle; the fixed-order and two-kernel losses equal
+    # the default path's.
+    B, H, W, T, sigma, kind = random_case(i)
+    params, bgs = make_case(B, H, W, T, kind, seed=300 + 10 * i)
+    targets = orc.render_batch(synth.batch(kind, B, T, 300 + 10 * i, target_offset=1000), H, W, sigma,
+                               bgs[::-1].copy())
+    print(f"random case {i}: B={B} H={H} W={W} T={T} sigma={sigma:.3g} kind={kind}", flush=True)
+    cl, cg = orc.loss_backward_batch(params, targets, sigma, bgs)
+    cimg = orc.render_batch(params, H, W, sigma, bgs)
+    losses = {}
+    for exact in (False, True):
+        gl, gg, gimg = ctx.fused_loss_backward(params, targets, sigma, bgs, exact=exact, want_images=True)
+        check_image(gimg, cimg, label=f"case {i} exact={exact}")
+        check_losses(gl, cl, label=f"case {i} exact={exact}")
+        assert_grads(gg, cg, label=f"case {i} exact={exact}")
+        losses[exact] = gl
+    dl, dg = ctx.fused_loss_backward(params, targets, sigma, bgs, deterministic=True)
+    assert np.array_equal(dl, losses[False])
+    assert_grads(dg, cg, label=f"case {i} fixed-order")
+    monkeypatch.setenv("DRH_UNFUSED", "1")
+    ul, ug = ctx.fused_loss_backward(params, targets, sigma, bgs)
+    assert np.array_equal(ul, losses[False])
+    assert_grads(ug, cg, label=f"case {i} two kernels")
