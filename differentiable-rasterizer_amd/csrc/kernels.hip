@@ -603,11 +603,23 @@ enum : uint32_t { ENT_INBOX = 0x20 };
 // edges are strictly farther (by a margin well above rounding) at every pixel,
 // so the reference's first-minimum selection picks j with the same distance,
 // and the inside test reduces to the sign of c_j.
-// The edge's fields come from its block of the record (rp, wave-uniform), one
-// scalar load at an offset set by the plan.
-__device__ inline Geo geometry1(const Rec& r, const float* __restrict__ rp, Pix p, uint32_t plan) {
+// The record's block of the plan's edge (R_EB + 8 j, j = plan & 3; the
+// general plan's 3 reads edge 2's block, unused), loaded by the fast-path
+// sweeps together with the record: the asm keeps the load where it is, so its
+// scalar round trip is the record's instead of a second one inside the exact
+// path. In bounds for every record: R_EB + 24 == REC.
+static_assert(R_EB + 24 == REC, "three 8-float edge blocks end the record");
+template <bool FAST>
+__device__ inline f8v edge_block(const float* __restrict__ rp, uint32_t plan) {
+    if (!FAST) return f8v{};
+    f8v eb = *reinterpret_cast<const f8v*>(rp + R_EB + 8 * min(plan & 3u, 2u));
+    asm volatile("" : "+s"(eb));
+    return eb;
+}
+
+// The edge's fields come from its block of the record (edge_block).
+__device__ inline Geo geometry1(const Rec& r, const f8v& eb, Pix p, uint32_t plan) {
     const int j = (int)(plan & 3u);
-    const f8v eb = *reinterpret_cast<const f8v*>(rp + R_EB + 8 * j);
     const float ax = eb[0], ay = eb[1], ex = eb[2], ey = eb[3], len2 = eb[4], rl = eb[5];
     const float apx = p.px - ax, apy = p.py - ay;
     const float c = ex * apy - ey * apx;
@@ -635,11 +647,11 @@ __device__ inline Geo geometry1(const Rec& r, const float* __restrict__ rp, Pix 
 // and on the plan are wave-uniform; the empty volatile asm keeps the compiler
 // from if-converting them, which would evaluate every variant every time.
 template <bool FAST>
-__device__ inline void exact_cov(const Rec& r, const float* __restrict__ rp, Pix p, uint32_t plan, float rsig,
-                                 float sig, Geo& g, float& cov) {
+__device__ inline void exact_cov(const Rec& r, const f8v& eb, Pix p, uint32_t plan, float rsig, float sig, Geo& g,
+                                 float& cov) {
     if (FAST && (r.i(R_FLAGS) & F_FAST)) {
         if ((plan & 3u) != PLAN_GENERAL) {
-            g = geometry1(r, rp, p, plan);
+            g = geometry1(r, eb, p, plan);
         } else {
             asm volatile("");
             g = geometry<true>(r, p);
@@ -908,7 +920,7 @@ classify:
 // predicates rather than branches; only the exact path is a (divergent)
 // branch, so the wave runs it once for the lanes that need it.
 template <bool FAST>
-__device__ inline uint64_t pair_weight(const Rec& r, const float* __restrict__ rp, uint32_t ent, int x, int y,
+__device__ inline uint64_t pair_weight(const Rec& r, const f8v& eb, uint32_t ent, int x, int y,
                                        Pix p, uint64_t validm, float& w, float& cov, uint64_t& bandm, Geo& g,
                                        float rsig, float sig) {
     const float alpha = r.f(R_A);
@@ -933,7 +945,7 @@ __device__ inline uint64_t pair_weight(const Rec& r, const float* __restrict__ r
         // pixel (more than 17 sigma + slack inside every edge line) gets
         // exp(-x) < 2^-24 and coverage exactly 1.0f, as classified; a far one
         // (beyond `far`) a weight below MIN_WEIGHT, skipped as classified.
-        g = geometry1(r, rp, p, (ent >> 2) & 7u);
+        g = geometry1(r, eb, p, (ent >> 2) & 7u);
         cov = sigmoid_f<true>(g.sd * rsig);
         w = alpha * cov;
         bandm = actm & lane_mask(cov != 1.0f);
@@ -948,7 +960,7 @@ __device__ inline uint64_t pair_weight(const Rec& r, const float* __restrict__ r
         g = geometry<true>(r, p);
         cov = sigmoid_f<true>(g.sd * rsig);
     } else if (__builtin_amdgcn_inverse_ballot_w64(bandm)) {
-        exact_cov<FAST>(r, rp, p, (ent >> 2) & 7u, rsig, sig, g, cov);
+        exact_cov<FAST>(r, eb, p, (ent >> 2) & 7u, rsig, sig, g, cov);
     }
     w = alpha * cov;
     // `bandm` hands the backward pass the lanes whose coverage it must evaluate:
@@ -1174,10 +1186,11 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
             const int k = kbase + (int)(ent >> 8);
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
+            const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
             float w = 0.0f, cov;
             uint64_t bandm;
             Geo g;
-            const uint64_t onm = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+            const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
             const bool on = __builtin_amdgcn_inverse_ballot_w64(onm);
             // MODE_RECORD draws what a render draws but hands over what the
             // taped forward keeps (F_TAPE); in the other modes the two agree.
@@ -1437,9 +1450,10 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
+            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
             float cov = 1.0f;
             Geo g;
-            if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
@@ -1483,10 +1497,11 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
                 const int kl = (int)(ent >> 8);
                 const float* rp = rec + (size_t)(k0 + kl) * REC;
                 const Rec r = load_rec(rp);
+                const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
                 float w = 0.0f, cov = 0.0f;
                 uint64_t bandm;
                 Geo g;
-                const uint64_t onm = pair_weight<FAST>(r, rp, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+                const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
                 if (onm == 0) continue;
                 bandm &= onm;
                 const bool any_band = bandm != 0;
@@ -1785,9 +1800,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             const float* rp = rec + (size_t)k * REC;
             const Rec r = load_rec(rp);
+            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
             float cov = 1.0f;
             Geo g;
-            if (band) exact_cov<FAST>(r, rp, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
