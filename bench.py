@@ -21,6 +21,7 @@ fit at 176x176, T=150, against the oracle's fit on one core).
     python bench.py [--steps K] [--warmup W] [--gpus 1]
     python bench.py --copy-calibration     # plain device copy, for PMC scaling
     python bench.py --crossover            # GPU vs this host's CPU over the reference's crossover cells
+    python bench.py --config c3 --no-cpu-baseline --steps 20 --warmup 5   # one workload alone
 """
 
 from __future__ import annotations
@@ -126,12 +127,18 @@ def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev, two_kernels=False)
     return {"setup": ms["setup"], "forward": ms["raster"], "backward": ms["backward"], "reduce": ms["reduce"]}
 
 
-def traffic_from_profiles(kernel):
-    """HBM bytes per launch of `kernel` from the committed PMC summary, if any."""
-    f = ROOT / "profiles" / "raster_kernels_c2_pmc.md"
+def pmc_profile(config):
+    return ROOT / "profiles" / f"raster_kernels_{config}_pmc.md"
+
+
+def traffic_from_profiles(kernel, config="c2"):
+    """HBM bytes per launch of `kernel` at `config`, read from the committed PMC
+    summary of that workload (a counter run of an earlier invocation, not this
+    run's measurement), or None."""
+    f = pmc_profile(config)
     if not f.exists():
         return None
-    m = re.search(kernel + r" traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    m = re.search(re.escape(kernel) + r" traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
     return float(m.group(1)) if m else None
 
 
@@ -179,7 +186,13 @@ def cpu_baseline(cfg, params, targets_np, budget_s):
 
 def fit_config(ctx, with_cpu=True):
     """Config c4: the device fit loop, 800 iterations at 176x176, T=150, against the
-    oracle's fit of the same start on one core (fit.rs:243-288 is sequential)."""
+    oracle's fit of the same start on one core (fit.rs:243-288 is sequential).
+    Throughput is dense pixel x triangle evaluations per second over the whole
+    fit (800 H W T / seconds). Its roofline is the fixed-order fused kernel's:
+    the fit's algorithmic FLOP (148 N_box + 61 N_contrib + 15 H W summed over
+    the iterations, the counts from the oracle's fit of the same start) per
+    launch, over that kernel's event-timed average duration in a fit run of its
+    own (timing on)."""
     from diffrast import synth
 
     cfg = synth.CONFIGS["c4"]
@@ -193,22 +206,42 @@ def fit_config(ctx, with_cpu=True):
         r = ctx.fit(target, init, bg, iters=iters, patience=None)
         runs.append(time.perf_counter() - t0)
     dt = float(np.median(runs))
+    ctx.timing(True)
+    try:
+        ctx.fit(target, init, bg, iters=iters, patience=None)
+        t = ctx.read_timings()
+    finally:
+        ctx.timing(False)
+    kt = {"setup": t["setup_ms"] / max(t["setup_n"], 1), "fused": t["raster_ms"] / max(t["raster_n"], 1),
+          "fit_step": t["adam_ms"] / max(t["adam_n"], 1)}
+    dense = iters * H * W * T
     out = dict(workload=f"device fit loop, B=1 {H}x{W} T={T}, {iters} iterations (patience off), "
                         "sigma 0.02 -> 0.0015, Adam lr 0.004/0.02/0.01",
                iterations=len(r["losses"]), seconds=round(dt, 4), ms_per_iteration=dt * 1e3 / iters,
+               pixel_tri_per_s=dense / dt, kernel_ms={k: round(v, 5) for k, v in kt.items()},
+               launches={"fused": t["raster_n"]},
                first_loss=float(r["losses"][0]), best_loss=r["best_loss"], best_iter=r["best_iter"],
                improvement=float(r["losses"][0] / r["best_loss"]))
     if with_cpu:
         from oracle import oracle
 
+        counts = oracle.Counts()
         t0 = time.perf_counter()
-        c = oracle.fit(target, init, bg, iters=iters, patience=None)
+        c = oracle.fit(target, init, bg, iters=iters, patience=None, counts=counts)
         cpu_s = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": iters / cpu_s, "unit": "iterations/s", "cores": 1, "kind": "port",
+        out["cpu_baseline"] = {"value": dense / cpu_s, "unit": UNIT, "cores": 1, "kind": "port",
                                "sample": f"the whole {iters}-iteration fit once, one thread",
                                "seconds": round(cpu_s, 3), "ms_per_iteration": cpu_s * 1e3 / iters,
+                               "iterations_per_s": iters / cpu_s,
                                "best_loss": c["best_loss"], "best_iter": c["best_iter"]}
         out["speedup_gpu_over_cpu"] = cpu_s / dt
+        flop = (FLOP_FWD[0] + FLOP_BWD[0]) * counts.n_box + (FLOP_FWD[1] + FLOP_BWD[1]) * counts.n_contrib \
+            + FLOP_FWD[2] * iters * H * W
+        out["roofline"] = roof("fused_kernel (fixed order)", flop / iters, kt["fused"],
+                               traffic_from_profiles("fused_kernel", "c4"))
+        out["roofline"]["n_box_pairs_all_iterations"] = int(counts.n_box)
+        out["roofline"]["n_contrib_pairs_all_iterations"] = int(counts.n_contrib)
+        out["roofline_step"] = roof("whole iteration (wall)", flop / iters, dt * 1e3 / iters)
     return out
 
 
@@ -332,13 +365,15 @@ def roof(kernel, flop, ms_k, traffic=None):
         "unit": "TFLOP/s",
         "frac": achieved / PEAK_FP32_TFLOPS,
         "traffic": traffic,
+        "traffic_source": "committed PMC summary under profiles/ (FETCH_SIZE, WRITE_SIZE), not this run"
+                          if traffic is not None else None,
         "kernel": kernel,
         "flop_per_launch": flop,
         "ms_per_launch": ms_k,
     }
 
 
-def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic=False):
+def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic=True):
     """One batched workload: wall ms per fused step, per-kernel event times, and (with
     `cpu`) the oracle's counts, parity, rooflines and the same-run CPU baseline."""
     from diffrast import synth
@@ -389,15 +424,15 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
     flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
     def two_kernel_roofs(k):
         return {"roofline_backward": roof("backward_kernel", flop_b, k["backward"],
-                                          traffic_from_profiles("backward_kernel") if traffic else None),
+                                          traffic_from_profiles("backward_kernel", name) if traffic else None),
                 "roofline_forward": roof("forward_kernel", flop_f, k["forward"],
-                                         traffic_from_profiles("forward_kernel") if traffic else None),
+                                         traffic_from_profiles("forward_kernel", name) if traffic else None),
                 "roofline_pair": roof("forward_kernel+backward_kernel", flop_f + flop_b,
                                       k["forward"] + k["backward"])}
 
     if "fused" in kt:
         out["roofline"] = roof("fused_tile_kernel", flop_f + flop_b, kt["fused"],
-                               traffic_from_profiles("fused_tile_kernel") if traffic else None)
+                               traffic_from_profiles("fused_tile_kernel", name) if traffic else None)
         two.update(two_kernel_roofs(two["kernel_ms"]))
         two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
         out["two_kernel_path"] = two
@@ -477,6 +512,8 @@ def main():
     ap.add_argument("--no-side", action="store_true", help="skip the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--crossover", action="store_true")
+    ap.add_argument("--config", choices=["c0", "c1", "c2", "c3", "c4"],
+                    help="measure this one workload alone and print its line (for profiling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -498,6 +535,14 @@ def main():
     log("device:", ctx.device_info())
     if args.crossover:
         crossover(torch, ctx, dev)
+        return
+    if args.config:
+        cpu = not args.no_cpu_baseline
+        if args.config == "c4":
+            one = fit_config(ctx, with_cpu=cpu)
+        else:
+            one = measure_batch(torch, ctx, args.config, dev, args.steps, args.warmup, cpu, args.cpu_budget)
+        print(json.dumps({"config": args.config, "steps": args.steps, "warmup": args.warmup, **one}), flush=True)
         return
     cfg = synth.CONFIGS["c2"]
     B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]

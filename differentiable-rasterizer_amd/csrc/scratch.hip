@@ -10,10 +10,17 @@
 // In host code `scratch` is a host-side stand-in for the array, not a device
 // address: scratch_init takes the device address once per device (with that
 // device current) and only that address is used afterwards. Every call on a
-// GPU shares that GPU's array, so calls that overlap on one GPU race.
+// GPU shares that GPU's array, so the calls on one GPU are serialized: a call
+// enqueues its launches under that GPU's mutex and then records the GPU's
+// event on its stream, and a call on another stream first makes its stream
+// wait for that event. Calls from several threads and streams therefore run
+// one after another on the device. Under graph capture no event is recorded or
+// waited for (an event of an eager call cannot order a graph's replays): the
+// caller orders the replays of a captured call against other calls.
 
 #include <hip/hip_runtime.h>
 
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -28,12 +35,22 @@ static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
 
 namespace {
 
-std::mutex g_mu;
-std::vector<void*> g_addr;  // device address of `scratch`, per device
+// One per device: the device address of `scratch` and what orders the calls
+// that share it.
+struct DeviceSlot {
+    void* addr = nullptr;
+    std::mutex call;             // held while a call enqueues its launches
+    hipEvent_t done = nullptr;   // recorded after the last call's last launch
+    hipStream_t last = nullptr;  // the stream it was recorded on
+    bool recorded = false;
+};
 
-void* scratch_addr(int device) {
+std::mutex g_mu;
+std::vector<std::unique_ptr<DeviceSlot>> g_dev;
+
+DeviceSlot* device_slot(int device) {
     std::lock_guard<std::mutex> g(g_mu);
-    return device >= 0 && (size_t)device < g_addr.size() ? g_addr[device] : nullptr;
+    return device >= 0 && (size_t)device < g_dev.size() ? g_dev[device].get() : nullptr;
 }
 
 // Offsets of the buffers of one call in the scratch array, each at a 256-byte
@@ -82,12 +99,16 @@ namespace drh_rt {
 
 int scratch_init(int device) {
     std::lock_guard<std::mutex> g(g_mu);
-    if ((size_t)device >= g_addr.size()) g_addr.resize((size_t)device + 1, nullptr);
-    if (g_addr[device]) return DRH_OK;
-    void* p = nullptr;
-    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
-    g_addr[device] = p;
+    if (device < 0) return fail(DRH_ERR_DEVICE, "no device");
+    if ((size_t)device >= g_dev.size()) g_dev.resize((size_t)device + 1);
+    if (g_dev[device]) return DRH_OK;
+    auto d = std::make_unique<DeviceSlot>();
+    hipError_t e = hipGetSymbolAddress(&d->addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !d->addr)
+        return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    e = hipEventCreateWithFlags(&d->done, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreate (scratch)");
+    g_dev[device] = std::move(d);
     return DRH_OK;
 }
 
@@ -115,8 +136,16 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
                                            "entry point that allocates nothing has " +
                                            std::to_string(SCRATCH_BYTES) + " (use drh_fused_loss_backward)");
     DeviceGuard dg(ctx->device);
-    char* base = static_cast<char*>(scratch_addr(ctx->device));
-    if (!base) return fail(DRH_ERR_DEVICE, "scratch array not initialised on this device");
+    DeviceSlot* d = device_slot(ctx->device);
+    if (!d) return fail(DRH_ERR_DEVICE, "scratch array not initialised on this device");
+    char* base = static_cast<char*>(d->addr);
+    hipStream_t s = (hipStream_t)stream;
+    // one call at a time per device: see the head of this file
+    std::lock_guard<std::mutex> one(d->call);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing");
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    if (eager && d->recorded && d->last != s) HIP_TRY(hipStreamWaitEvent(s, d->done, 0), "hipStreamWaitEvent (scratch)");
     RasterBufs bufs;
     bufs.rec = reinterpret_cast<float*>(base + L.rec);
     bufs.ploss = reinterpret_cast<double*>(base + L.ploss);
@@ -132,10 +161,16 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
     // Nothing in the scratch array needs to start at zero: every buffer is
     // written by this call's kernels before it is read (the gradients are the
     // caller's output and setup_records clears them).
-    hipStream_t s = (hipStream_t)stream;
-    if ((rc = run_raster_bufs(ctx, drh::MODE_LOSS, params, backgrounds, targets, (int)B, (int)T, (int)H, (int)W,
-                              sigma, out_images, out_grads, out_losses, flags, bufs, s, nullptr, false)))
-        return rc;
+    rc = run_raster_bufs(ctx, drh::MODE_LOSS, params, backgrounds, targets, (int)B, (int)T, (int)H, (int)W, sigma,
+                         out_images, out_grads, out_losses, flags, bufs, s, nullptr, false);
+    if (eager) {
+        // also after a failed launch: whatever was enqueued is ordered before the next call
+        hipError_t e = hipEventRecord(d->done, s);
+        if (e != hipSuccess) return rc ? rc : hip_fail(e, "hipEventRecord (scratch)");
+        d->recorded = true;
+        d->last = s;
+    }
+    if (rc) return rc;
     if (flags & DRH_SYNC) HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
     return DRH_OK;
 }

@@ -126,9 +126,13 @@ def mean_color(image: np.ndarray) -> np.ndarray:
 def sample(image: np.ndarray, x: float, y: float) -> np.ndarray:
     """fit.rs:381-385 nearest-pixel sample, clamped to the canvas."""
     H, W = image.shape[0], image.shape[1]
-    px = int(np.clip(np.trunc(np.float32(x) * np.float32(W)), 0, W - 1))
-    py = int(np.clip(np.trunc(np.float32(y) * np.float32(H)), 0, H - 1))
-    return np.asarray(image[py, px], np.float32).copy()
+
+    def index(v: float, n: int) -> int:
+        # Rust's `as isize`: truncates toward zero, saturates, NaN -> 0
+        f = np.float32(v) * np.float32(n)
+        return 0 if np.isnan(f) else int(np.clip(np.trunc(f), 0, n - 1))
+
+    return np.asarray(image[index(y, H), index(x, W)], np.float32).copy()
 
 
 def seed_scene(target: np.ndarray, T: int, seed: int, seed_scale: float = 0.18):

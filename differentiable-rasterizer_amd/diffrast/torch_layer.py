@@ -324,17 +324,37 @@ def shutdown_gpu() -> bool:
 atexit.register(shutdown_gpu)
 
 
-def policy_prefers_gpu(batch: int, triangles: int, pixels: int, discrete: bool | None = None) -> bool:
-    """The reference's `device="auto"` size rule (crates/diffrast-py/src/lib.rs:138-147).
+# Pixel x triangle evaluations per call from which a discrete MI355X beats
+# this host's CPU on the fused loss + backward with host arrays in and out.
+# Measured on MI355X against 16 EPYC cores (batch 1-16, 16-256 pixels square,
+# 2-512 triangles): the CPU wins up to 32,768 evaluations (0.07x-0.88x), the
+# GPU from 131,072 on (2.5x-113x), single scenes included (1 x 64x64 x 32:
+# 2.5x; 1 x 128x128 x 64: 16.9x). Its fixed cost is ~0.17-0.2 ms per call
+# (copies, launch, wait) whatever the batch, so the rule has no batch term;
+# the floor sits at the log-midpoint of the crossover interval.
+MI355X_WORK_FLOOR = 65_536
 
-    Kept for API compatibility and answered with the reference's thresholds.
-    This build has no CPU backend, so `auto` runs on the GPU whatever the rule
-    says.
+
+def policy_prefers_gpu(batch: int, triangles: int, pixels: int, discrete: bool | None = None) -> bool:
+    """`device="auto"`'s size rule (crates/diffrast-py/src/lib.rs:113-147), re-derived for MI355X.
+
+    Discrete GPUs (the default): the GPU is worth it from `MI355X_WORK_FLOOR`
+    pixel x triangle evaluations per call, with no batch condition; the
+    reference's rule (batch >= 2 and >= 250,000, measured on an RTX 4090)
+    would send single scenes to the CPU that this GPU runs 2.5-17x faster.
+    Integrated GPUs keep the reference's rule (no integrated part was
+    measured here). The rule is advisory in this build: it has no CPU backend,
+    so `auto` runs on the GPU whatever the rule says.
     """
     if discrete is None:
         discrete = True
     if not discrete:
         return batch >= 4 and batch * triangles * pixels >= 1_000_000_000
+    return batch >= 1 and batch * triangles * pixels >= MI355X_WORK_FLOOR
+
+
+def _rtx4090_rule(batch: int, triangles: int, pixels: int) -> bool:
+    """The reference's discrete-GPU rule (crates/diffrast-py/src/lib.rs:138-147), for comparison."""
     return batch >= 2 and batch * triangles * pixels >= 250_000
 
 

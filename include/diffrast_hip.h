@@ -144,10 +144,13 @@ int drh_fused_loss_backward(drh_ctx *ctx, const float *params, const float *back
  * (DRH_HOST_PTRS is refused: staging would allocate). The call's buffers
  * besides its inputs and outputs live in a 128 MiB array that the library
  * holds on each GPU until the process ends; sizes whose buffers exceed it
- * (far beyond B=16 at 256x256, T=128) return DRH_ERR_TOO_LARGE. Calls that
- * overlap on one GPU share that array and race: the caller orders them (one
- * stream, or events). Results equal drh_fused_loss_backward's; its
- * launches are not counted by drh_timing_*. */
+ * (far beyond B=16 at 256x256, T=128) return DRH_ERR_TOO_LARGE. The calls
+ * on one GPU share that array, so the library runs them one after another:
+ * a call on another stream than the previous call's waits on the device for
+ * that call to finish (calls from several threads and streams are safe).
+ * Under graph capture that ordering is left to the caller: replays of a
+ * captured call must not overlap other calls on the same GPU. Results equal
+ * drh_fused_loss_backward's; its launches are not counted by drh_timing_*. */
 int drh_fused_loss_backward_noalloc(drh_ctx *ctx, const float *params, const float *backgrounds,
                                     const float *targets, int64_t B, int64_t T, int64_t H, int64_t W,
                                     float sigma, float *out_losses, float *out_grads, float *out_images,

@@ -597,10 +597,12 @@ void orc_sample(const float *image, size_t W, size_t H, float x, float y, float 
 }
 
 /* fit.rs:214-288 Fitter::new + Fitter::step, driven to completion as fit()
- * does (fit.rs:166-181), from a caller-supplied initial scene. */
+ * does (fit.rs:166-181), from a caller-supplied initial scene. counts (may be
+ * NULL) sums every iteration's box and contributing pairs. */
 void orc_fit(const float *target, size_t W, size_t H, const float bg[3],
              const float *init_params, size_t T, const orc_fit_config *cfg,
-             float *losses, float *best_params, orc_fit_report *report) {
+             float *losses, float *best_params, orc_fit_report *report,
+             orc_counts *counts) {
     size_t np = T * NP;
     float *params = (float *)malloc((np ? np : 1) * sizeof(float));
     float *grads = (float *)malloc((np ? np : 1) * sizeof(float));
@@ -627,7 +629,7 @@ void orc_fit(const float *target, size_t W, size_t H, const float bg[3],
         }
         size_t i = iter;
         float sigma = orc_sigma_at(cfg->sigma_start, cfg->sigma_end, cfg->iters, i);
-        float loss = orc_loss_backward(params, T, bg, W, H, sigma, target, grads, NULL, NULL);
+        float loss = orc_loss_backward(params, T, bg, W, H, sigma, target, grads, NULL, counts);
         if (!isfinite(loss)) {
             stop = ORC_DIVERGED;
             break;

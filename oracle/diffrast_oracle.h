@@ -112,7 +112,8 @@ typedef struct {
  * cfg->iters floats; best_params T*10 floats. */
 void orc_fit(const float *target, size_t W, size_t H, const float bg[3],
              const float *init_params, size_t T, const orc_fit_config *cfg,
-             float *losses, float *best_params, orc_fit_report *report);
+             float *losses, float *best_params, orc_fit_report *report,
+             orc_counts *counts);
 
 /* fit.rs:369-385 mean_color() and sample(), used by seed_scene(). */
 void orc_mean_color(const float *image, size_t W, size_t H, float out[3]);

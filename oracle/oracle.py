@@ -86,7 +86,7 @@ def lib() -> ctypes.CDLL:
         L.orc_sigma_at.argtypes = [ctypes.c_float, ctypes.c_float, _SZ, _SZ]
         L.orc_sigma_at.restype = ctypes.c_float
         L.orc_fit.argtypes = [_F, _SZ, _SZ, _F, _F, _SZ, ctypes.POINTER(FitConfig), _F, _F,
-                              ctypes.POINTER(FitReport)]
+                              ctypes.POINTER(FitReport), C]
         L.orc_mean_color.argtypes = [_F, _SZ, _SZ, _F]
         L.orc_sample.argtypes = [_F, _SZ, _SZ, ctypes.c_float, ctypes.c_float, _F]
         L.orc_signed_distance.argtypes = [_F, ctypes.c_float, ctypes.c_float]
@@ -273,11 +273,12 @@ FIT_DEFAULTS = dict(iters=1500, sigma_start=0.02, sigma_end=0.0015, lr_pos=0.004
                     lr_color=0.02, lr_alpha=0.01, patience=250, min_delta=1e-7)
 
 
-def fit(target, init_params, background=None, **cfg):
+def fit(target, init_params, background=None, counts=None, **cfg):
     """fit.rs:166-288 from a given initial scene.
 
     Returns dict(losses, best_params, best_iter, best_loss, stop_reason).
-    `patience=None` disables early stopping (fit.rs:60-62).
+    `patience=None` disables early stopping (fit.rs:60-62). `counts` (a
+    Counts) sums the box and contributing pairs of every iteration.
     """
     c = dict(FIT_DEFAULTS)
     c.update(cfg)
@@ -292,7 +293,7 @@ def fit(target, init_params, background=None, **cfg):
     best = np.empty_like(p)
     rep = FitReport()
     lib().orc_fit(_p(t), W, H, _p(bg), _p(p), p.shape[0], ctypes.byref(conf), _p(losses),
-                  _p(best), ctypes.byref(rep))
+                  _p(best), ctypes.byref(rep), ctypes.byref(counts) if counts is not None else None)
     return dict(losses=losses[: rep.n_losses].copy(), best_params=best, best_iter=rep.best_iter,
                 best_loss=float(rep.best_loss), stop_reason=STOP_REASONS[rep.stop_reason])
 

@@ -137,14 +137,14 @@ int main(void) {
         orc_fit_config cfg = {30, 0.02f, 0.0015f, 0.004f, 0.02f, 0.01f, -1, 1e-7f};
         float *losses = xmalloc(sizeof(float) * 30), *best = xmalloc(sizeof(float) * n);
         orc_fit_report rep;
-        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep);
+        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep, NULL);
         cfg.patience = 3;
-        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep);
+        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep, NULL);
         cfg.iters = 0;
-        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep);
+        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep, NULL);
         cfg.iters = 10;
         target[5] = nanf("");
-        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep);
+        orc_fit(target, W, H, bg, p, T, &cfg, losses, best, &rep, NULL);
         free(p), free(grads), free(lr), free(m), free(v), free(target), free(losses), free(best);
     }
     /* sRGB both ways, every byte and a scan of the encoding */

@@ -118,6 +118,11 @@ def test_c4_fit_800_iterations(ctx, orc):
           f"all {rel.max():.2e}; best gpu {g['best_loss']:.6e} @{g['best_iter']} "
           f"oracle {c['best_loss']:.6e} @{c['best_iter']}", flush=True)
     assert rel[:20].max() <= 1e-4
+    # the trajectories stay together: the first 100 losses, and the best
+    # snapshot (iteration and loss) as the reference's loop picks it
+    assert rel[:100].max() <= 1e-3
+    assert g["best_iter"] == c["best_iter"]
+    assert abs(g["best_loss"] - c["best_loss"]) <= 1e-3 * c["best_loss"]
     # the best snapshot is the scene its loss was measured on, at that iteration's sigma
     sig = orc.sigma_at(0.02, 0.0015, iters, g["best_iter"])
     again = orc.mse(orc.render(g["best_params"], H, W, sig, bg), target)

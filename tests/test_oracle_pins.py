@@ -260,3 +260,32 @@ def test_mean_color_and_sample(orc):
     assert np.array_equal(synth.mean_color(img), orc.mean_color(img))
     for x, y in [(0.0, 0.0), (0.999, 0.5), (1.5, -0.3), (0.51, 0.49)]:
         assert np.array_equal(orc.sample(img, x, y), synth.sample(img, x, y))
+
+
+def test_sample_truncates_toward_zero_and_clamps(orc):
+    # fit.rs:381-385: `(x * W as f32) as isize`, clamped to [0, W - 1]; Rust's
+    # float-to-int cast truncates toward zero, saturates, and sends NaN to 0.
+    # The image stores each pixel's own column and row, so the sample names
+    # the pixel it read.
+    H, W = 7, 11
+    img = np.zeros((H, W, 3), np.float32)
+    img[..., 0] = np.arange(W, dtype=np.float32)[None, :]
+    img[..., 1] = np.arange(H, dtype=np.float32)[:, None]
+    img[..., 2] = 5.0
+    nan, inf = float("nan"), float("inf")
+    cases = [  # (x, y, column, row)
+        (0.0, 0.0, 0, 0),
+        (0.5, 0.5, 5, 3),              # 5.5 and 3.5 truncate; x scales by W, y by H
+        (2.99 / W, 4.999 / H, 2, 4),   # truncation, not rounding
+        (-0.05, -0.1, 0, 0),           # -0.55 and -0.7 truncate to 0
+        (-0.5, -3.0, 0, 0),            # negative: clamped to 0
+        (1.0, 1.0, W - 1, H - 1),      # exactly 1: W and H, clamped to the last pixel
+        (1.5, 2.0, W - 1, H - 1),      # above 1: clamped
+        (nan, nan, 0, 0),              # NaN casts to 0
+        (inf, -inf, W - 1, 0),         # saturating casts
+        (0.95, 0.0, 10, 0),            # 10.45 -> 10
+    ]
+    for x, y, cx, cy in cases:
+        got = orc.sample(img, x, y)
+        assert got.tolist() == [float(cx), float(cy), 5.0], (x, y, got)
+        assert np.array_equal(synth.sample(img, x, y), got), (x, y)

@@ -255,13 +255,24 @@ def test_fused_mse_rejects_bad_shapes():  # test_torch_layer.py:273-278
 
 
 # ---------------------------------------------------------------- policy
-# The reference's `device="auto"` rule pinned to its measured crossovers
-# (docs/gpu-report.txt via test_torch_layer.py:281-351): GPU-over-CPU
-# speedups at batch 16; cells within +/-10% are ties and skipped. This build
-# runs "auto" on the GPU whatever the rule says; the rule is kept for callers
-# that query it.
+# `device="auto"`'s rule pinned to measured crossovers, as the reference pins
+# its own (test_torch_layer.py:281-351): GPU-over-CPU speedups, cells within
+# +/-10% are ties and skipped. The discrete rule is pinned to this GPU's table;
+# the reference's RTX 4090 and integrated tables stay pinned to the rules they
+# were measured for. This build runs "auto" on the GPU whatever the rule says.
 
-DISCRETE = [
+# MI355X against 16 EPYC host cores, the fused loss + backward with host arrays
+# in and out (bench.py --crossover): (batch, pixels, triangles, speedup).
+MI355X = [
+    (16, 64 * 64, 32, 4.89), (16, 64 * 64, 128, 9.19), (16, 64 * 64, 512, 22.98),
+    (16, 128 * 128, 32, 7.19), (16, 128 * 128, 128, 22.43), (16, 128 * 128, 512, 62.10),
+    (16, 256 * 256, 32, 12.76), (16, 256 * 256, 128, 41.66), (16, 256 * 256, 512, 113.04),
+    (1, 16 * 16, 2, 0.07), (1, 32 * 32, 8, 0.23), (2, 32 * 32, 16, 0.88),
+    (1, 64 * 64, 32, 2.48), (2, 64 * 64, 32, 3.08), (4, 64 * 64, 64, 5.54),
+    (1, 128 * 128, 64, 16.89),
+]
+# The reference's tables at batch 16 (docs/gpu-report.txt): RTX 4090, and an integrated AMD 860M.
+RTX4090 = [
     (64 * 64, 32, 1.85), (64 * 64, 128, 1.70), (64 * 64, 512, 2.26),
     (128 * 128, 32, 4.06), (128 * 128, 128, 4.96), (128 * 128, 512, 3.89),
     (256 * 256, 32, 3.64), (256 * 256, 128, 6.03), (256 * 256, 512, 3.89),
@@ -273,19 +284,42 @@ INTEGRATED = [
 ]
 
 
-@pytest.mark.parametrize("discrete,table", [(True, DISCRETE), (False, INTEGRATED)],
-                         ids=["discrete", "integrated"])
-def test_policy_matches_the_crossover_tables(discrete, table):
-    for pixels, tris, speedup in table:
+def test_policy_matches_the_mi355x_crossover():
+    for batch, pixels, tris, speedup in MI355X:
         if 0.9 <= speedup <= 1.1:
             continue
-        assert policy_prefers_gpu(16, tris, pixels, discrete) == (speedup > 1.0), (pixels, tris)
+        assert policy_prefers_gpu(batch, tris, pixels, True) == (speedup > 1.0), (batch, pixels, tris)
 
 
-def test_single_images_and_trivial_workloads_stay_on_the_cpu():  # test_torch_layer.py:331-341
-    assert not policy_prefers_gpu(1, 512, 256 * 256, True)
+def test_policy_floor_lies_inside_the_measured_crossover():
+    from diffrast.torch_layer import MI355X_WORK_FLOOR
+
+    cpu_wins = max(b * p * t for b, p, t, s in MI355X if s < 0.9)
+    gpu_wins = min(b * p * t for b, p, t, s in MI355X if s > 1.1)
+    assert cpu_wins < MI355X_WORK_FLOOR <= gpu_wins
+
+
+def test_reference_rules_match_their_tables():
+    from diffrast.torch_layer import _rtx4090_rule
+
+    for pixels, tris, speedup in RTX4090:
+        assert _rtx4090_rule(16, tris, pixels) == (speedup > 1.0), (pixels, tris)
+    for pixels, tris, speedup in INTEGRATED:
+        assert policy_prefers_gpu(16, tris, pixels, False) == (speedup > 1.0), (pixels, tris)
+
+
+def test_single_images_and_trivial_workloads():  # test_torch_layer.py:331-341
+    # the reference keeps single images on the CPU (its 4090 rule); on MI355X a
+    # single 256x256 scene of 512 triangles is far past the work floor
+    from diffrast.torch_layer import _rtx4090_rule
+
+    assert not _rtx4090_rule(1, 512, 256 * 256)
+    assert policy_prefers_gpu(1, 512, 256 * 256, True)
     assert policy_prefers_gpu(16, 512, 256 * 256, True)
+    # below the floor the fixed cost of a call dominates
     assert not policy_prefers_gpu(4, 8, 16 * 16, True)
+    assert not policy_prefers_gpu(1, 2, 16 * 16, True)
+    assert not policy_prefers_gpu(0, 512, 256 * 256, True)
 
 
 # ---------------------------------------------------------------- helpers

@@ -93,3 +93,58 @@ def test_noalloc_takes_no_pool_buffer_and_refuses_what_it_cannot_do():
                               losses.data_ptr(), grads.data_ptr(), None, s, 0)
     assert e.value.code == 5 and "scratch" in str(e.value)
     ctx.close()
+
+
+def test_noalloc_calls_from_two_threads_on_two_streams():
+    # The calls on one GPU share its scratch array; the library runs them one
+    # after another, so calls made concurrently from two host threads on two
+    # streams return what the pooled entry point returns, bit for bit with
+    # fixed-order sums. Every job has the same sizes (only the scenes differ).
+    import threading
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    ctx = _lib.Context()
+    s0 = torch.cuda.current_stream(dev).cuda_stream
+    B, H, W, T = 4, 96, 80, 64
+    jobs = []
+    for j in range(8):
+        p = torch.from_numpy(synth.batch("uniform", B, T, 100 + j)).to(dev)
+        tp = torch.from_numpy(synth.batch("uniform", B, T, 100 + j, target_offset=1000)).to(dev)
+        bg = torch.zeros((B, 3), device=dev)
+        tg = torch.empty((B, H, W, 3), device=dev)
+        ctx.render_ptr(tp.data_ptr(), bg.data_ptr(), B, T, H, W, SIGMA, tg.data_ptr(), s0)
+        want_l, want_g = torch.empty(B, device=dev), torch.empty((B, T, 10), device=dev)
+        ctx.fused_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), B, T, H, W, SIGMA, want_l.data_ptr(),
+                      want_g.data_ptr(), None, s0, _lib.DETERMINISTIC)
+        got_l = torch.full((B,), float("nan"), device=dev)
+        got_g = torch.full((B, T, 10), float("nan"), device=dev)
+        jobs.append((p, bg, tg, want_l, want_g, got_l, got_g))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(dev) for _ in range(2)]  # default priority
+    errors = []
+
+    def worker(k):
+        s = streams[k].cuda_stream
+        try:
+            for rep in range(3):
+                for j in range(k, len(jobs), 2):
+                    p, bg, tg, _, _, got_l, got_g = jobs[j]
+                    ctx.fused_noalloc_ptr(p.data_ptr(), bg.data_ptr(), tg.data_ptr(), B, T, H, W, SIGMA,
+                                          got_l.data_ptr(), got_g.data_ptr(), None, s, _lib.DETERMINISTIC)
+        except Exception as e:  # reported below, not swallowed
+            errors.append(repr(e))
+
+    print(f"noalloc: two threads on two streams, {len(jobs)} jobs x 3, B={B} {H}x{W} T={T}", flush=True)
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for j, (_, _, _, want_l, want_g, got_l, got_g) in enumerate(jobs):
+        assert torch.equal(got_l, want_l), j
+        assert torch.equal(got_g, want_g), j
+    ctx.close()
