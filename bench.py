@@ -18,6 +18,11 @@ baseline (the C oracle, one thread per scene, on this host's cores), and under
 headline), c3 (B=8 256x256 T=512 small triangles) and c4 (the 800-iteration
 fit at 176x176, T=150, against the oracle's fit on one core).
 
+The headline is measured first in the process, then every other GPU leg, then
+the CPU legs. The GPU's clocks ramp up over ~18 ms of sustained load (the c2
+step from ~111 to ~100 us), so with a few warm-up steps the headline runs in
+that ramp; "sustained" reports the same step after 200 untimed steps beside it.
+
     python bench.py [--steps K] [--warmup W] [--gpus 1]
     python bench.py --copy-calibration     # plain device copy, for PMC scaling
     python bench.py --crossover            # GPU vs this host's CPU over the reference's crossover cells
@@ -184,15 +189,11 @@ def cpu_baseline(cfg, params, targets_np, budget_s):
                 n_box=int(counts.n_box), n_contrib=int(counts.n_contrib))
 
 
-def fit_config(ctx, with_cpu=True):
-    """Config c4: the device fit loop, 800 iterations at 176x176, T=150, against the
-    oracle's fit of the same start on one core (fit.rs:243-288 is sequential).
-    Throughput is dense pixel x triangle evaluations per second over the whole
-    fit (800 H W T / seconds). Its roofline is the fixed-order fused kernel's:
-    the fit's algorithmic FLOP (148 N_box + 61 N_contrib + 15 H W summed over
-    the iterations, the counts from the oracle's fit of the same start) per
-    launch, over that kernel's event-timed average duration in a fit run of its
-    own (timing on)."""
+def fit_gpu(ctx):
+    """Config c4 on the GPU: the device fit loop, 800 iterations at 176x176, T=150
+    (fit.rs:243-288), three timed fits after a short warm-up, then one with the
+    kernels event-timed. Throughput is dense pixel x triangle evaluations per
+    second over the whole fit (800 H W T / seconds)."""
     from diffrast import synth
 
     cfg = synth.CONFIGS["c4"]
@@ -214,35 +215,54 @@ def fit_config(ctx, with_cpu=True):
         ctx.timing(False)
     kt = {"setup": t["setup_ms"] / max(t["setup_n"], 1), "fused": t["raster_ms"] / max(t["raster_n"], 1),
           "fit_step": t["adam_ms"] / max(t["adam_n"], 1)}
-    dense = iters * H * W * T
     out = dict(workload=f"device fit loop, B=1 {H}x{W} T={T}, {iters} iterations (patience off), "
                         "sigma 0.02 -> 0.0015, Adam lr 0.004/0.02/0.01",
                iterations=len(r["losses"]), seconds=round(dt, 4), ms_per_iteration=dt * 1e3 / iters,
-               pixel_tri_per_s=dense / dt, kernel_ms={k: round(v, 5) for k, v in kt.items()},
+               pixel_tri_per_s=iters * H * W * T / dt, kernel_ms={k: round(v, 5) for k, v in kt.items()},
                launches={"fused": t["raster_n"]},
                first_loss=float(r["losses"][0]), best_loss=r["best_loss"], best_iter=r["best_iter"],
                improvement=float(r["losses"][0] / r["best_loss"]))
-    if with_cpu:
-        from oracle import oracle
+    log(f"c4: {dt * 1e3 / iters:.4f} ms/iteration; kernel avg ms {kt}")
+    return out, dict(target=target, init=init, bg=bg, dt=dt, kt=kt)
 
-        counts = oracle.Counts()
-        t0 = time.perf_counter()
-        c = oracle.fit(target, init, bg, iters=iters, patience=None, counts=counts)
-        cpu_s = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": dense / cpu_s, "unit": UNIT, "cores": 1, "kind": "port",
-                               "sample": f"the whole {iters}-iteration fit once, one thread",
-                               "seconds": round(cpu_s, 3), "ms_per_iteration": cpu_s * 1e3 / iters,
-                               "iterations_per_s": iters / cpu_s,
-                               "best_loss": c["best_loss"], "best_iter": c["best_iter"]}
-        out["speedup_gpu_over_cpu"] = cpu_s / dt
-        flop = (FLOP_FWD[0] + FLOP_BWD[0]) * counts.n_box + (FLOP_FWD[1] + FLOP_BWD[1]) * counts.n_contrib \
-            + FLOP_FWD[2] * iters * H * W
-        out["roofline"] = roof("fused_kernel (fixed order)", flop / iters, kt["fused"],
-                               traffic_from_profiles("fused_kernel", "c4"))
-        out["roofline"]["n_box_pairs_all_iterations"] = int(counts.n_box)
-        out["roofline"]["n_contrib_pairs_all_iterations"] = int(counts.n_contrib)
-        out["roofline_step"] = roof("whole iteration (wall)", flop / iters, dt * 1e3 / iters)
+
+def fit_cpu(out, keep):
+    """Config c4 on the CPU, after fit_gpu: the oracle's fit of the same start on
+    one core, timed; its pair counts give the fit's algorithmic FLOP (148 N_box +
+    61 N_contrib + 15 H W summed over the iterations), and the roofline is the
+    fixed-order fused kernel's: that FLOP per launch over its event-timed
+    average duration."""
+    from diffrast import synth
+    from oracle import oracle
+
+    cfg = synth.CONFIGS["c4"]
+    H, W, T, iters = cfg["H"], cfg["W"], cfg["T"], cfg["iters"]
+    dt, kt = keep["dt"], keep["kt"]
+    dense = iters * H * W * T
+    counts = oracle.Counts()
+    t0 = time.perf_counter()
+    c = oracle.fit(keep["target"], keep["init"], keep["bg"], iters=iters, patience=None, counts=counts)
+    cpu_s = time.perf_counter() - t0
+    out["cpu_baseline"] = {"value": dense / cpu_s, "unit": UNIT, "cores": 1, "kind": "port",
+                           "sample": f"the whole {iters}-iteration fit once, one thread",
+                           "seconds": round(cpu_s, 3), "ms_per_iteration": cpu_s * 1e3 / iters,
+                           "iterations_per_s": iters / cpu_s,
+                           "best_loss": c["best_loss"], "best_iter": c["best_iter"]}
+    out["speedup_gpu_over_cpu"] = cpu_s / dt
+    flop = (FLOP_FWD[0] + FLOP_BWD[0]) * counts.n_box + (FLOP_FWD[1] + FLOP_BWD[1]) * counts.n_contrib \
+        + FLOP_FWD[2] * iters * H * W
+    out["roofline"] = roof("fused_kernel (fixed order)", flop / iters, kt["fused"],
+                           traffic_from_profiles("fused_kernel", "c4"))
+    out["roofline"]["n_box_pairs_all_iterations"] = int(counts.n_box)
+    out["roofline"]["n_contrib_pairs_all_iterations"] = int(counts.n_contrib)
+    out["roofline_step"] = roof("whole iteration (wall)", flop / iters, dt * 1e3 / iters)
     return out
+
+
+def fit_config(ctx, with_cpu=True):
+    """fit_gpu, then (with_cpu) fit_cpu."""
+    out, keep = fit_gpu(ctx)
+    return fit_cpu(out, keep) if with_cpu else out
 
 
 def torch_op_ms(torch, cfg, p, targets, dev, steps=50):
@@ -334,15 +354,26 @@ def forward_side(torch, ctx, dev, cpu=True):
         host_ms = (time.perf_counter() - t0) * 1e3 / 5
         res[name] = {"B": B, "H": H, "W": W, "T": T, "sigma": sig, "ms": round(dev_ms, 4),
                      "host_ms": round(host_ms, 4), "pixel_tri_per_s": B * H * W * T / (dev_ms / 1e3)}
-        if cpu and name == "fwd_512_T1024":
-            from oracle import oracle
-
-            t0 = time.perf_counter()
-            oracle.render_batch(params, H, W, sig, bg, nthreads=1)
-            cpu_ms = (time.perf_counter() - t0) * 1e3
-            res[name]["cpu_oracle_1thread_ms"] = round(cpu_ms, 2)
-            res[name]["speedup_vs_cpu_1thread"] = round(cpu_ms / dev_ms, 1)
+        if name == "fwd_512_T1024":
+            res[name]["_inputs"] = (params, bg)
+    if cpu:
+        forward_cpu(res)
     return res
+
+
+def forward_cpu(res):
+    """The oracle's single-thread render of the 512x512 T=1024 cell, beside forward_side's GPU time."""
+    from oracle import oracle
+
+    r = res.get("fwd_512_T1024")
+    if not r or "_inputs" not in r:
+        return
+    params, bg = r.pop("_inputs")
+    t0 = time.perf_counter()
+    oracle.render_batch(params, r["H"], r["W"], r["sigma"], bg, nthreads=1)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    r["cpu_oracle_1thread_ms"] = round(cpu_ms, 2)
+    r["speedup_vs_cpu_1thread"] = round(cpu_ms / r["ms"], 1)
 
 
 def copy_calibration(torch):
@@ -373,9 +404,10 @@ def roof(kernel, flop, ms_k, traffic=None):
     }
 
 
-def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic=True):
-    """One batched workload: wall ms per fused step, per-kernel event times, and (with
-    `cpu`) the oracle's counts, parity, rooflines and the same-run CPU baseline."""
+def gpu_leg(torch, ctx, name, dev, steps, warmup, two_kernels=True):
+    """The GPU side of one batched workload: wall ms per fused step over `steps`
+    calls after `warmup`, per-kernel event times, and (two_kernels) the same step
+    on the two-kernel path. Returns the config's line and what cpu_leg needs."""
     from diffrast import synth
 
     cfg = synth.CONFIGS[name]
@@ -386,7 +418,7 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
     log(f"{name}: {ms:.4f} ms/batch over {steps} steps; kernel avg ms {kt}")
     # the same step on the two-kernel path, for its per-kernel figures
     two = None
-    if "fused" in kt:
+    if "fused" in kt and two_kernels:
         os.environ["DRH_UNFUSED"] = "1"
         try:
             ms2 = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)[0]
@@ -400,28 +432,40 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
         "workload": f"batched soft-raster forward+MSE+backward, B={B} {H}x{W} T={T} sigma={SIGMA}"
                     + (" (small triangles)" if cfg["kind"] == "small" else ""),
         "B": B, "H": H, "W": W, "T": T,
+        "steps": steps, "warmup": warmup,
         "ms_per_batch": ms,
         "pixel_tri_per_s": dense / (ms / 1e3),
         "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
     }
-    if not cpu:
-        return out
-    targets_np = targets.cpu().numpy()
-    c = cpu_baseline(cfg, params, targets_np, cpu_budget)
+    keep = dict(name=name, cfg=cfg, params=params, targets_np=targets.cpu().numpy(),
+                losses=losses.cpu().numpy(), grads=grads.cpu().numpy(), kt=kt, two=two)
+    return out, keep
+
+
+def cpu_leg(out, keep, cpu_budget, traffic=True):
+    """The CPU side of one batched workload, after its gpu_leg: the oracle on the
+    same batch (parity figures, N_box and N_contrib), the rooflines of the GPU
+    leg's kernels and the same-run CPU baseline."""
+    name, cfg, kt, two = keep["name"], keep["cfg"], keep["kt"], keep["two"]
+    B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
+    ms = out["ms_per_batch"]
+    dense = B * H * W * T
+    c = cpu_baseline(cfg, keep["params"], keep["targets_np"], cpu_budget)
     log(f"{name}: cpu baseline {c['per_batch_s'] * 1e3:.1f} ms/batch on {c['threads']} threads")
-    g = grads.cpu().numpy().reshape(B, -1, 10).astype(np.float64)
+    g = keep["grads"].reshape(B, -1, 10).astype(np.float64)
     cg = c["grads"].reshape(B, -1, 10).astype(np.float64)
     par = {"grad_max_abs_over_norm": max(float(np.abs(g[b] - cg[b]).max() / np.linalg.norm(cg[b]))
                                          for b in range(B))}
     for gname, sl in GROUPS.items():
         par[f"grad_{gname}"] = max(float(np.abs(g[b][:, sl] - cg[b][:, sl]).max() /
                                          max(np.linalg.norm(cg[b][:, sl]), 1e-30)) for b in range(B))
-    l = losses.cpu().numpy().astype(np.float64)
+    l = keep["losses"].astype(np.float64)
     par["loss_rel"] = float(np.max(np.abs(l - c["losses"]) / np.abs(c["losses"])))
     out["parity_vs_oracle"] = par
     counts = (c["n_box"], c["n_contrib"], B * H * W)
     flop_f = sum(a * b for a, b in zip(FLOP_FWD, counts))
     flop_b = sum(a * b for a, b in zip(FLOP_BWD, counts))
+
     def two_kernel_roofs(k):
         return {"roofline_backward": roof("backward_kernel", flop_b, k["backward"],
                                           traffic_from_profiles("backward_kernel", name) if traffic else None),
@@ -433,9 +477,10 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
     if "fused" in kt:
         out["roofline"] = roof("fused_tile_kernel", flop_f + flop_b, kt["fused"],
                                traffic_from_profiles("fused_tile_kernel", name) if traffic else None)
-        two.update(two_kernel_roofs(two["kernel_ms"]))
-        two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
-        out["two_kernel_path"] = two
+        if two is not None:
+            two.update(two_kernel_roofs(two["kernel_ms"]))
+            two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
+            out["two_kernel_path"] = two
     else:
         r = two_kernel_roofs(kt)
         out["roofline"] = r.pop("roofline_backward")
@@ -459,6 +504,12 @@ def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic
         "speedup_gpu_over_cpu": c["per_batch_s"] * 1e3 / ms,
     }
     return out
+
+
+def measure_batch(torch, ctx, name, dev, steps, warmup, cpu, cpu_budget, traffic=True):
+    """gpu_leg, then (with `cpu`) cpu_leg."""
+    out, keep = gpu_leg(torch, ctx, name, dev, steps, warmup)
+    return cpu_leg(out, keep, cpu_budget, traffic) if cpu else out
 
 
 def crossover(torch, ctx, dev):
@@ -547,7 +598,42 @@ def main():
     cfg = synth.CONFIGS["c2"]
     B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
     cpu = not args.no_cpu_baseline
-    head = measure_batch(torch, ctx, "c2", dev, args.steps, args.warmup, cpu, args.cpu_budget, traffic=True)
+    # Order of the run: every GPU leg first, then the CPU legs (the oracle),
+    # during which the GPU idles:
+    # - the headline: c2 with `warmup` untimed and `steps` timed steps, first
+    #   thing in the process;
+    # - the other configurations' GPU legs (c0, c1, c3, the c4 fit);
+    # - "sustained": the same c2 step again after 200 more untimed steps (the
+    #   GPU's clocks ramp up over ~18 ms of sustained load), reported beside
+    #   the headline, not as it;
+    # - the torch-op and forward-only side measurements.
+    head, head_keep = gpu_leg(torch, ctx, "c2", dev, args.steps, args.warmup)
+    legs, fit = {}, None
+    if not args.no_side:
+        for name in ("c0", "c1", "c3"):
+            legs[name] = gpu_leg(torch, ctx, name, dev, 20, 5)
+        fit = fit_gpu(ctx)
+    sustained, _ = gpu_leg(torch, ctx, "c2", dev, 100, 200, two_kernels=False)
+    side = {}
+    if not args.no_side:
+        p = torch.from_numpy(synth.batch("uniform", B, T, 1)).to(dev)
+        _, _, _, targets = make_inputs(torch, ctx, cfg, 1, dev)
+        side["c2_torch_fused_mse_fwd_bwd_ms"] = round(torch_op_ms(torch, cfg, p, targets, dev), 4)
+        side["c2_torch_rasterize_mse_fwd_bwd_ms"] = round(torch_rasterize_ms(torch, cfg, p, targets, dev), 4)
+        side["c2_torch_rasterize_mse_fwd_bwd_rerender_ms"] = round(
+            torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=False), 4)
+        side["forward_only"] = forward_side(torch, ctx, dev, cpu=False)
+    # the CPU legs
+    if cpu:
+        head = cpu_leg(head, head_keep, args.cpu_budget)
+        for name, (o, k) in legs.items():
+            legs[name] = (cpu_leg(o, k, args.cpu_budget), k)
+        if fit is not None:
+            fit = (fit_cpu(*fit), None)
+        if not args.no_side:
+            forward_cpu(side["forward_only"])
+    for r in side.get("forward_only", {}).values():
+        r.pop("_inputs", None)
     ms = head["ms_per_batch"]
     dense = B * H * W * T
     out = {
@@ -571,25 +657,23 @@ def main():
         "roofline_step": head.get("roofline_step"),
         "two_kernel_path": head.get("two_kernel_path"),
         "cpu_baseline": head.get("cpu_baseline"),
+        "sustained": {"ms_per_step": sustained["ms_per_batch"], "kernel_ms": sustained["kernel_ms"],
+                      "steps": 100, "warmup": 200,
+                      "note": "the same step measured again later in the run, after 200 untimed steps: the GPU's "
+                              "clocks ramp up over ~18 ms of sustained load, so a training loop runs at this "
+                              "rate; the headline above keeps the requested warm-up"},
     }
+    if "roofline" in head and cpu:
+        flop = head["roofline"]["flop_per_launch"]
+        out["sustained"]["roofline_frac"] = flop / (sustained["kernel_ms"]["fused"] / 1e3) / 1e12 / PEAK_FP32_TFLOPS
+        out["sustained"]["roofline_step_frac"] = flop / (sustained["ms_per_batch"] / 1e3) / 1e12 / PEAK_FP32_TFLOPS
     if not args.no_side:
-        configs = {}
-        for name in ("c0", "c1"):
-            configs[name] = measure_batch(torch, ctx, name, dev, 20, 5, cpu, args.cpu_budget)
+        configs = {name: legs[name][0] for name in ("c0", "c1")}
         configs["c2"] = head
-        configs["c3"] = measure_batch(torch, ctx, "c3", dev, 20, 5, cpu, args.cpu_budget)
-        configs["c4"] = fit_config(ctx, with_cpu=cpu)
+        configs["c3"] = legs["c3"][0]
+        configs["c4"] = fit[0]
         out["configs"] = configs
-        p = torch.from_numpy(synth.batch("uniform", B, T, 1)).to(dev)
-        _, _, _, targets = make_inputs(torch, ctx, cfg, 1, dev)
-        side = {}
-        side["c2_torch_fused_mse_fwd_bwd_ms"] = round(torch_op_ms(torch, cfg, p, targets, dev), 4)
-        side["c2_torch_rasterize_mse_fwd_bwd_ms"] = round(torch_rasterize_ms(torch, cfg, p, targets, dev), 4)
-        side["c2_torch_rasterize_mse_fwd_bwd_rerender_ms"] = round(
-            torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=False), 4)
-        side["forward_only"] = forward_side(torch, ctx, dev, cpu=cpu)
         out["side"] = side
-
     print(json.dumps(out), flush=True)
 
 

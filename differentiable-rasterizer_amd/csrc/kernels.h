@@ -59,6 +59,11 @@ enum : int { SETUP_RENDER = 0, SETUP_TAPE = 1, SETUP_RECORD = 2 };
 // reclassifies its remaining chunks there.
 constexpr int CAP2_MIN = 128;
 
+// fused_seg_kernel: waves per tile, and the most triangles per scene (its LDS
+// holds a 288-byte record per entry of the tile: 46 KB at 160).
+constexpr int SEG_WAVES = 4;
+constexpr int SEG_MAX_T = 160;
+
 // One recorded entry of a tile's list, written by the forward kernel and read
 // (with scalar loads) by the backward kernel.
 struct TileEnt {
@@ -122,6 +127,10 @@ struct RasterArgs {
     int2* pze;             // ntiles*64 zero and rescaling counts (irregular tiles)
     TileEnt* tl_ent;       // ntiles*cap2 recorded entries
     int cap2;              // entries recorded per tile
+    // fused_seg_kernel's waves per tile (SEG_WAVES), or 0: the fused path
+    // takes the other kernels. cap2 is then SEG_WAVES x a multiple of 8, and
+    // with DRH_DETERMINISTIC the partial rows and loss partials are per tile.
+    int segw;
     int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded | TN_IRREGULAR
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)
@@ -201,8 +210,10 @@ struct FitTail {
 };
 
 dim3 raster_grid(int B, int W, int H);
-hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int T, double npix3,
-                           const FitTail& ft, hipStream_t s);
+// nblk partial rows (and loss partials) per scene, loss_per of which form a
+// block's loss (1, or WAVES for fused_seg_kernel's per-tile rows).
+hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int loss_per, int T,
+                           double npix3, const FitTail& ft, hipStream_t s);
 // bg_dst (optional) receives a copy of the B x 3 backgrounds at bg_src; with
 // o.cnt, the block order is made (OrderArgs).
 // halt (optional): the kernel does nothing once *halt >= 0 (a stopped fit).
@@ -227,7 +238,7 @@ hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int pe
 // Loss partials per block that a gradient call's raster kernels write.
 constexpr int loss_partials_per_block(bool fused, bool deterministic) { return fused && !deterministic ? WAVES : 1; }
 // npix3: 3 H W, the divisor of the per-item loss (canvas.rs:45-58)
-hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
+hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int loss_per, int T,
                          double npix3, float* grads, float* losses, hipStream_t s, const int* halt = nullptr);
 // 256 floats passed by value to the sRGB kernels: the byte thresholds of the
 // encoding (entry k the smallest linear value whose byte is k; entry 0 unused)

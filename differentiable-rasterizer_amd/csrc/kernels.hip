@@ -1141,17 +1141,21 @@ __device__ inline TileGeo tile_geo_split(int W, int H, int gx, int gy, const int
 // split backward's checkpoints too. lw: the wave's LDS list. MERGE: lists of
 // merged chunks (build_list), for a caller that takes every triangle index from
 // the recorded entries; rec_chunks is then meaningless.
+// [kbeg, kend) (merged lists without ROWS only; default all of them): the
+// triangles swept, and ent_off: where in the tile's region the entries go (a
+// segment of fused_seg_kernel).
 template <int MODE, bool FAST, bool CKPT, bool MERGE = false, bool ROWS = false>
 __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* __restrict__ rec, const TileGeo& tg,
                                               uint64_t validm, float rsig, float sig, uint32_t* lw,
-                                              float (&col)[3], Trans& tot, int& n2, int& rec_chunks) {
+                                              float (&col)[3], Trans& tot, int& n2, int& rec_chunks,
+                                              int kbeg = 0, int kend = -1, int ent_off = 0) {
     const int T = a.T, lane = tg.lane;
     const int n_chunks = (T + CH - 1) / CH;
     n2 = 0;                 // contributing entries seen (recorded while n2 < cap2)
     rec_chunks = n_chunks;  // chunks whose contributing entries are all recorded
     const int cap2 = a.cap2;
     // wave-uniform: the entry stores address from a scalar base
-    TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
+    TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2 + ent_off;
     // Split backward: before recorded entry (c + 1) seg_m the pixel state goes to
     // checkpoint c of this tile, the start of the backward's segment c + 1 (of
     // the blocks the backward splits: those ranked below nsplit, or all
@@ -1165,13 +1169,13 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
     static_assert(MERGE || !ROWS, "row lists are merged lists");
     // ROWS: merged lists over the tile row's triangles, which setup_records listed
     const int* ilist = nullptr;
-    int nlist = T;
+    int nlist = kend < 0 ? T : kend;
     if (ROWS) {
         const size_t row = (size_t)tg.b * a.row_gy + (tg.ty0 >> 3);
         ilist = a.rows + row * T;
         nlist = a.row_n[row];
     }
-    int k1 = 0;
+    int k1 = MERGE ? kbeg : 0;
     for (int c = 0; MERGE ? k1 < nlist : c < n_chunks; c++) {
         const int k0 = MERGE ? k1 : c * CH;
         k1 = MERGE ? nlist : min(T, k0 + CH);
@@ -1816,6 +1820,222 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
         sweep(std::false_type{});
 }
 
+// Grids of few tiles (a single scene of a few hundred 8x8 tiles, the fit):
+// one tile per workgroup of S waves. Where the one-wave kernel runs about one
+// wave per SIMD and is bound by the chain of dependent waits per entry of its
+// tile (scalar record loads, LDS round trips), this one splits the tile's
+// triangles over the waves, wave s taking [s T / S, (s + 1) T / S):
+//  A. each wave lists its triangles and evaluates their weights at the tile's
+//     pixels (pair_weight: the exact path, the classification), records its
+//     entries for the backward, and leaves each entry's weights, colour and
+//     contributing lanes in LDS;
+//  B. every wave composites all the tile's entries from LDS in scene order
+//     (raster.rs:37-68), exactly as the one-wave kernel's forward sweep does,
+//     so the image, the transmittance and the loss are the same bits; a wave
+//     keeps the canvas and the transmittance at the start of its segment;
+//  C. each wave sweeps its own entries backward from that state, as the
+//     one-wave kernel sweeps all of them.
+// The tile's entry region (cap2 = S x capS entries) holds segment s's entries
+// at s capS. DET: each wave sums its entries' gradients into LDS rows of its
+// segment's triangles and the tile writes its partial rows (B x tiles x T x
+// NP) for reduce_partials / fit_step; otherwise each entry's wave sum goes to
+// the gradients as float atomics. The loss partial is per tile either way,
+// summed four to a 16x16 block first, as sum_losses sums the one-wave
+// kernel's.
+//
+// Dynamic LDS: phases A and B hold cap2 SegEnt records; phase C reuses the
+// same area for the waves' transposition areas (and DET accumulator rows).
+struct SegEnt {
+    float w[64];       // weight at each lane's pixel
+    float c[3];        // colour
+    uint32_t on[2];    // lanes it contributes at (low, high word)
+    uint32_t pad[3];
+};
+static_assert(sizeof(SegEnt) == 288 && sizeof(SegEnt) % 16 == 0, "SegEnt keeps 16-byte alignment");
+constexpr int SEG_MAX = SEG_MAX_T / SEG_WAVES;  // triangles per segment
+
+// Phase C's LDS bytes, and the workgroup's dynamic LDS.
+__host__ __device__ constexpr size_t seg_lds_c(bool det, int cap_s) {
+    return (size_t)SEG_WAVES * NP * TP * sizeof(float) + (det ? (size_t)SEG_WAVES * cap_s * NP * sizeof(float) : 0);
+}
+__host__ __device__ constexpr size_t seg_lds_bytes(bool det, int cap2) {
+    return (size_t)cap2 * sizeof(SegEnt) > seg_lds_c(det, cap2 / SEG_WAVES) ? (size_t)cap2 * sizeof(SegEnt)
+                                                                              : seg_lds_c(det, cap2 / SEG_WAVES);
+}
+
+template <int MODE, bool FAST, bool DET, int S>
+__global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const float* __restrict__ records,
+                                                          const TileEnt* __restrict__ ents) {
+    static_assert(MODE == MODE_LOSS || MODE == MODE_GRAD_IN, "gradient modes only");
+    static_assert(S == SEG_WAVES, "seg_lds_bytes sizes the LDS for SEG_WAVES waves");
+    __shared__ uint32_t list[S][CH];
+    __shared__ int nent[S];
+    extern __shared__ __attribute__((aligned(16))) float seg_lds[];
+    SegEnt* const sent = reinterpret_cast<SegEnt*>(seg_lds);
+    if (a.halt && *a.halt >= 0) return;
+    const int W = a.W, H = a.H, T = a.T;
+    const int s = (int)uniform_u32(threadIdx.x >> 6);  // this wave's segment
+    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0);
+    const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
+    const int lane = tg.lane, b = tg.b;
+    const float sig = fmaxf(a.sigma, 1e-8f);
+    const float rsig = a.rsig;
+    const float* __restrict__ rec = records + (size_t)b * T * REC;
+    const int k0 = (int)(((long long)s * T) / S), k1 = (int)(((long long)(s + 1) * T) / S);
+    const int capS = a.cap2 / S;
+    // wave-uniform: the entry stores and loads address from a scalar base
+    TileEnt* const te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * a.cap2 + s * capS;
+
+    // A. the segment's entries and their weights
+    int n2 = 0;
+    for (int kb = k0; kb < k1;) {
+        int kend;
+        const int count = tg.live ? build_list<true>(rec, kb, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
+                                                     tg.cx1, tg.cy1, list[s], lane, F_LIVE, &kend)
+                                  : 0;
+        const int kbase = kb;
+        kb = tg.live ? kend : k1;
+        uint32_t nxt = list[s][0];  // the next entry is read one iteration ahead
+        for (int i = 0; i < count; i++) {
+            const uint32_t ent = uniform_u32(nxt);
+            nxt = list[s][min(i + 1, CH - 1)];
+            const int k = kbase + (int)(ent >> 8);
+            const float* rp = rec + (size_t)k * REC;
+            const Rec r = load_rec(rp);
+            const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
+            float w = 0.0f, cov;
+            uint64_t bandm;
+            Geo g;
+            const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+            if (onm == 0) continue;  // wave-uniform
+            SegEnt& e = sent[s * capS + n2];
+            e.w[lane] = w;
+            if (lane == 0) {
+                e.c[0] = r.f(R_C);
+                e.c[1] = r.f(R_C + 1);
+                e.c[2] = r.f(R_C + 2);
+                e.on[0] = (uint32_t)onm;
+                e.on[1] = (uint32_t)(onm >> 32);
+                TileEnt t;
+                t.k = ((uint32_t)k << 8) | (ent & 0xFFu);
+                t.row = 0;
+                t.on = onm;
+                t.band = onm & bandm;
+                te[n2] = t;
+            }
+            n2++;
+        }
+    }
+    if (lane == 0) nent[s] = n2;
+    // The entries were recorded with vector stores and are read back below with
+    // scalar loads: the stores are complete (in L2, which the scalar cache reads
+    // from) before any of those loads issue (the regions are whole cache lines).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // B. the tile's composite in scene order, forward_sweep's arithmetic
+    Back st;
+    float col[3];
+    Trans tot = {1.0f, 0, 0};
+    for (int ch = 0; ch < 3; ch++) col[ch] = a.bg[b * 3 + ch];
+    for (int q = 0; q < S; q++) {
+        if (q == s) {
+            for (int ch = 0; ch < 3; ch++) st.col[ch] = col[ch];
+            st.pre = tot;
+        }
+        const int n = nent[q];
+        for (int i = 0; i < n; i++) {
+            const SegEnt& e = sent[q * capS + i];
+            const float w = e.w[lane];
+            const bool on = ((lane < 32 ? e.on[0] >> lane : e.on[1] >> (lane - 32)) & 1u) != 0;
+            const float omw = 1.0f - w;
+            for (int ch = 0; ch < 3; ch++) {
+                const float o = fmaf(w, e.c[ch] - col[ch], col[ch]);
+                col[ch] = on ? o : col[ch];
+            }
+            const float f = on ? omw : 1.0f;
+            const float qn = tot.q * f;
+            if (lane_mask(!(qn >= 5.421010862427522e-20f)) == 0)
+                tot.q = qn;
+            else
+                trans_mul(tot, f);
+        }
+    }
+    st.tot = tot;
+    if (MODE == MODE_LOSS && a.out_img && tg.valid && s == 0)
+        for (int ch = 0; ch < 3; ch++) a.out_img[img_index(a, tg.pix, b, ch)] = col[ch];
+    for (int ch = 0; ch < 3; ch++) st.g0[ch] = 0.0f;
+    double l = 0.0;
+    if (tg.valid) {
+        if (MODE == MODE_LOSS) {
+            // the loss (canvas.rs:45-58) and dL/dpixel (grad.rs:111-114) as forward_kernel forms them
+            const float scale = a.lscale;
+            for (int ch = 0; ch < 3; ch++) {
+                float t = a.target[img_index(a, tg.pix, b, ch)];
+                float d = col[ch] - t;
+                l += (double)d * (double)d;
+                st.g0[ch] = scale * (col[ch] - t);
+            }
+        } else {
+            for (int ch = 0; ch < 3; ch++) st.g0[ch] = a.grad_in[img_index(a, tg.pix, b, ch)];
+        }
+    }
+    if (MODE == MODE_LOSS && s == 0) {
+        l = wave_sum_f64(l);
+        if (lane == 0) a.partial_loss[tg.tile] = l;
+    }
+    const bool plain = lane_mask(tot.z != 0 || tot.e != 0) == 0;  // the same in every wave
+    __syncthreads();  // phase C reuses the SegEnt area
+
+    // C. this segment's entries backward
+    lds_float* const tw = (lds_float*)(seg_lds + s * (NP * TP));
+    lds_float* const accs = (lds_float*)(seg_lds + S * (NP * TP) + s * (capS * NP));
+    if (DET) {
+        for (int j = lane; j < capS * NP; j += 64) accs[j] = 0.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
+    const TileEnt* __restrict__ tr = te;
+    float* const grads = DET ? nullptr : a.grads + (size_t)b * T * NP;
+    auto sweep = [&](auto plain_c) {
+        constexpr bool PLAIN = decltype(plain_c)::value;
+        TileEnt nx = tr[0];
+        for (int i2 = 0; i2 < n2; i2++) {
+            const TileEnt cur = nx;
+            const int k = (int)(cur.k >> 8);
+            nx = tr[min(i2 + 1, capS - 1)];
+            const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
+            const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
+            const float* rp = rec + (size_t)k * REC;
+            const Rec r = load_rec(rp);
+            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
+            float cov = 1.0f;
+            Geo g;
+            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            const float w = r.f(R_A) * cov;
+            float part[NP];
+            grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
+            if (DET)
+                reduce_entry(part, tw, accs + (k - k0) * NP, lane);
+            else
+                reduce_entry_global(part, tw, grads + (size_t)k * NP, lane);
+        }
+    };
+    if (plain)
+        sweep(std::true_type{});
+    else
+        sweep(std::false_type{});
+    if (DET) {
+        // the tile's partial rows of this segment's triangles
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float* prow = a.partials + ((size_t)tg.tile * T + k0) * NP;
+        for (int j = lane; j < (k1 - k0) * NP; j += 64) prow[j] = accs[j];
+    }
+}
+
 // Lane `lane`'s share of a scene's block loss sums: blocks lane, lane + 64, ...
 // added in turn to a double, each block's PER partials summed in order first.
 // The loads of SUM_UNROLL blocks are issued before any of them is added, so up
@@ -1876,9 +2096,15 @@ __global__ __launch_bounds__(64) void sum_losses(const double* __restrict__ part
 // (scene, 64 columns); its 16 waves each sum a contiguous range of rows
 // (sum_rows_in_order), and the ranges are combined in row order.
 constexpr int RED_WAVES = 16;
+// loss_per: loss partials per block (1, or WAVES when the rows and partials
+// are per tile: fused_seg_kernel), summed per block first as sum_losses does.
+__device__ inline double scene_loss(const double* __restrict__ pl, int nrows, int loss_per, int lane) {
+    return loss_per == WAVES ? lane_block_losses<WAVES>(pl, nrows / WAVES, lane)
+                             : lane_block_losses<1>(pl, nrows, lane);
+}
 __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* __restrict__ partials,
                                                                   const double* __restrict__ partial_loss,
-                                                                  int nblk, int T, double npix3,
+                                                                  int nblk, int loss_per, int T, double npix3,
                                                                   float* __restrict__ grads,
                                                                   float* __restrict__ losses,
                                                                   const int* __restrict__ halt) {
@@ -1900,7 +2126,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void reduce_partials(const float* _
         grads[(size_t)b * cols + col] = v;
     }
     if (losses && blockIdx.x == 0 && wave == 0) {
-        const double s = wave_sum_f64(lane_block_losses<1>(partial_loss + (size_t)b * nblk, nblk, lane));
+        const double s = wave_sum_f64(scene_loss(partial_loss + (size_t)b * nblk, nblk, loss_per, lane));
         if (lane == 0) losses[b] = (float)(s / npix3);
     }
 }
@@ -1942,7 +2168,7 @@ __global__ void adam_project(float* __restrict__ params, const float* __restrict
 // only carries the state forward (its raster kernels returned at entry).
 __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restrict__ partials,
                                                            const double* __restrict__ partial_loss, int nblk,
-                                                           int T, double npix3, FitTail ft) {
+                                                           int loss_per, int T, double npix3, FitTail ft) {
     __shared__ float part[RED_WAVES][64];
     __shared__ int decision;
     const FitState cur = ft.st[ft.iter & 1];
@@ -1970,7 +2196,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
         acc = sum_rows_in_order(partials + col, cols, (nblk * wave) / RED_WAVES, (nblk * (wave + 1)) / RED_WAVES);
     part[wave][lane] = acc;
     if (wave == 1) {
-        const double s = wave_sum_f64(lane_block_losses<1>(partial_loss, nblk, lane));
+        const double s = wave_sum_f64(scene_loss(partial_loss, nblk, loss_per, lane));
         if (lane == 0) {
             // fit.rs:243-288
             const float L = (float)(s / npix3);
@@ -2085,10 +2311,11 @@ hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const Sr
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int T, double npix3,
-                           const FitTail& ft, hipStream_t s) {
+hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int loss_per, int T,
+                           double npix3, const FitTail& ft, hipStream_t s) {
+    if (loss_per != 1 && (loss_per != WAVES || nblk % WAVES != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((T * NP + 63) / 64));
-    hipLaunchKernelGGL(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, T, npix3, ft);
+    hipLaunchKernelGGL(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T, npix3, ft);
     return hipGetLastError();
 }
 
@@ -2183,6 +2410,19 @@ static void launch_fused_d(bool fast, const RasterArgs& a, dim3 grid, hipStream_
 
 template <int MODE>
 static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
+    if (a.segw) {
+        const dim3 tiles(grid.x * grid.y * grid.z * WAVES), threads(SEG_WAVES * 64);
+        const size_t lds = seg_lds_bytes(a.deterministic != 0, a.cap2);
+        if (a.deterministic && fast)
+            hipLaunchKernelGGL((fused_seg_kernel<MODE, true, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+        else if (a.deterministic)
+            hipLaunchKernelGGL((fused_seg_kernel<MODE, false, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+        else if (fast)
+            hipLaunchKernelGGL((fused_seg_kernel<MODE, true, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+        else
+            hipLaunchKernelGGL((fused_seg_kernel<MODE, false, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+        return;
+    }
     if (a.deterministic) {
         launch_fused_d<MODE, true>(fast, a, grid, s);
         return;
@@ -2202,6 +2442,9 @@ static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
     if ((size_t)a.B * a.H * a.W == 0) return hipSuccess;
     if ((mode != MODE_LOSS && mode != MODE_GRAD_IN) || a.cap2 < a.T || a.cap2 % 8 != 0 || a.nseg > 1)
+        return hipErrorInvalidValue;
+    if (a.segw && (a.segw != SEG_WAVES || a.T > SEG_MAX_T || a.cap2 % (8 * SEG_WAVES) != 0 ||
+                   a.cap2 / SEG_WAVES < (a.T + SEG_WAVES - 1) / SEG_WAVES))
         return hipErrorInvalidValue;
     const dim3 grid = raster_grid(a.B, a.W, a.H);
     if (mode == MODE_LOSS)
@@ -2224,12 +2467,13 @@ hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int pe
     return hipGetLastError();
 }
 
-hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int T,
+hipError_t launch_reduce(const float* partials, const double* partial_loss, int B, int nblk, int loss_per, int T,
                          double npix3, float* grads, float* losses, hipStream_t s, const int* halt) {
+    if (loss_per != 1 && (loss_per != WAVES || nblk % WAVES != 0)) return hipErrorInvalidValue;
     int cols = T * NP;
     dim3 grid((cols + 63) / 64 > 0 ? (cols + 63) / 64 : 1, B);
-    hipLaunchKernelGGL(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, T, npix3,
-                       grads, losses, halt);
+    hipLaunchKernelGGL(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T,
+                       npix3, grads, losses, halt);
     return hipGetLastError();
 }
 

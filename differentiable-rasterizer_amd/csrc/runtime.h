@@ -242,7 +242,19 @@ struct RasterBufs {
     bool order_tiles = false;       // `order` ranks 8x8 tiles (one-wave fused kernel only), not blocks
     int* rows = nullptr;            // with order_tiles: B*2gy*T triangle indices per 8x8-tile row, or null
     int* row_n = nullptr;           // B*2gy counts
+    int segw = 0;                   // fused_seg_kernel's waves per tile (RasterArgs::segw), or 0
 };
+
+// fused_seg_kernel takes the gradient calls (fused, outside the split backward)
+// whose grids hold at most SEG_MAX_TILES 8x8 tiles, two per SIMD of the
+// device: there the one-wave kernel runs about one wave per SIMD, bound by
+// each tile's chain of dependent waits, and splitting a tile's triangles over
+// SEG_WAVES waves shortens that chain. From SEG_MIN_T triangles (a couple per
+// wave) up to drh::SEG_MAX_T. DRH_NO_SEGMENTS=1 in the environment keeps the
+// other fused kernels (for comparing the paths).
+constexpr size_t SEG_MAX_TILES = 2048;
+constexpr int SEG_MIN_T = 2 * drh::SEG_WAVES;
+bool use_segments(int mode, size_t ntiles, int T);
 
 // The one-wave fused kernel's lists scan the triangles of their tile row
 // (OrderArgs::rows) from this many triangles on. Below it a tile's box tests

@@ -296,6 +296,14 @@ bool fused_gradients(int mode, int nseg, int cap2, int T) {
     return !(e && e[0] == '1');
 }
 
+bool use_segments(int mode, size_t ntiles, int T) {
+    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || T < SEG_MIN_T || T > drh::SEG_MAX_T ||
+        ntiles > SEG_MAX_TILES)
+        return false;
+    const char* e = std::getenv("DRH_NO_SEGMENTS");
+    return !(e && e[0] == '1');
+}
+
 int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bgs, const float* img_in, int B,
                     int T, int H, int W, float sigma, float* out_img, float* out_grads, float* out_losses,
                     uint32_t flags, const RasterBufs& bufs, hipStream_t s, const int* halt, bool timed,
@@ -304,6 +312,8 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     const bool det = (flags & DRH_DETERMINISTIC) != 0;
     const dim3 grid = drh::raster_grid(B, W, H);
     const int nblk = (int)(grid.x * grid.y);
+    // fixed-order partial rows (and loss partials) per scene: per block, or per tile in fused_seg_kernel
+    const int nrows = bufs.segw ? nblk * drh::WAVES : nblk;
     drh::OrderArgs ord{};
     if (bufs.order)
         ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3, bufs.rows, bufs.row_n}
@@ -330,6 +340,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.pze = bufs.pze;
     a.tl_ent = bufs.tent;
     a.cap2 = bufs.cap2;
+    a.segw = bufs.fused ? bufs.segw : 0;
     a.tl_n = bufs.tn;
     a.grads = out_grads;
     a.losses = out_losses;
@@ -362,11 +373,13 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     }
     if (det && tail) {
         KernelTimer kt(ctx, TK_ADAM, s, timed);
-        HIP_TRY(drh::launch_fit_step(a.partials, a.partial_loss, nblk, T, 3.0 * (double)H * (double)W, *tail, s),
+        HIP_TRY(drh::launch_fit_step(a.partials, a.partial_loss, nrows, nrows / nblk, T, 3.0 * (double)H * (double)W,
+                                     *tail, s),
                 "fit_step launch");
     } else if (det) {
         KernelTimer kt(ctx, TK_REDUCE, s, timed);
-        HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nblk, T, 3.0 * (double)H * (double)W, out_grads,
+        HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nrows, nrows / nblk, T, 3.0 * (double)H * (double)W,
+                                   out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
                 "reduce_partials launch");
     } else if (bufs.fused && mode == drh::MODE_LOSS) {
@@ -410,6 +423,11 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         }
     }
     bufs.fused = fused_gradients(mode, bufs.nseg, bufs.cap2, T);
+    if (bufs.fused && use_segments(mode, ntiles, T)) {
+        // each wave's region whole 64-byte lines
+        bufs.segw = drh::SEG_WAVES;
+        bufs.cap2 = drh::SEG_WAVES * (((T + drh::SEG_WAVES - 1) / drh::SEG_WAVES + 7) & ~7);
+    }
     if (ordered) {
         // the one-wave fused kernel takes an order of tiles where its cells fit
         bufs.order_tiles = bufs.fused && !det &&
@@ -419,7 +437,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         bufs.order = order.get<int>();
         // the tile rows' triangle lists, where their bit masks fit setup_records' LDS
         const size_t trows = (size_t)B * 2 * grid.y;
-        if (bufs.order_tiles && T >= ROW_LISTS_MIN_T &&
+        if (bufs.order_tiles && !bufs.segw && T >= ROW_LISTS_MIN_T &&
             (size_t)2 * grid.y * ((T + 31) / 32) <= (size_t)drh::ORD_ROW_WORDS) {
             if ((rc = rows.acquire(ctx, K_ROWS, (trows * T + trows) * sizeof(int), s))) return rc;
             bufs.rows = rows.get<int>();
@@ -427,8 +445,8 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
         }
     }
     if (mode != drh::MODE_RENDER) {
-        if (det && (rc = partials.acquire(ctx, K_PARTIALS, (size_t)B * nblk * T * NP * sizeof(float), s)))
-            return rc;
+        const size_t prows = (size_t)B * nblk * (bufs.segw ? drh::WAVES : 1);  // per block, or per tile
+        if (det && (rc = partials.acquire(ctx, K_PARTIALS, prows * T * NP * sizeof(float), s))) return rc;
         if ((rc = ploss.acquire(ctx, K_PLOSS, (size_t)B * nblk * drh::WAVES * sizeof(double), s))) return rc;  // per tile
         if ((rc = tent.acquire(ctx, K_TILE_ENT, ntiles * bufs.cap2 * sizeof(drh::TileEnt), s))) return rc;
         // the hand-over between the two kernels (the fused kernel keeps it in registers)
@@ -942,7 +960,7 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     }
     if (det) {
         KernelTimer kt(ctx, TK_REDUCE, s);
-        HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, a.T, 3.0 * a.H * (double)a.W, grads.dev, nullptr, s),
+        HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, 1, a.T, 3.0 * a.H * (double)a.W, grads.dev, nullptr, s),
                 "reduce_partials launch");
     }
     if ((rc = copy_back(grads, s))) return rc;

@@ -60,6 +60,7 @@ DeviceSlot* device_slot(int device) {
 struct ScratchLayout {
     size_t rec = 0, ploss = 0, pq = 0, pg0 = 0, pze = 0, tn = 0, order = 0, partials = 0, tent = 0, total = 0;
     int cap2 = 0;
+    int segw = 0;  // fused_seg_kernel, as drh_fused_loss_backward takes it
     bool ordered = false;
 };
 
@@ -84,11 +85,20 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     L.ordered = use_order(ctx, B, (int)grid.x, (int)grid.y);
     L.order = off;
     if (L.ordered) off = up(off + (size_t)B * nblk * sizeof(int));
+    // the call takes fused_seg_kernel where drh_fused_loss_backward would
+    const int seg_cap2 = drh::SEG_WAVES * (((T + drh::SEG_WAVES - 1) / drh::SEG_WAVES + 7) & ~7);
+    L.segw = use_segments(drh::MODE_LOSS, ntiles, T) && fused_gradients(drh::MODE_LOSS, 1, seg_cap2, T)
+                 ? drh::SEG_WAVES
+                 : 0;
     L.partials = off;
-    if (det) off = up(off + (size_t)B * nblk * T * NP * sizeof(float));
+    if (det) off = up(off + (size_t)B * nblk * (L.segw ? drh::WAVES : 1) * T * NP * sizeof(float));
     L.tent = off;
     const size_t left = SCRATCH_BYTES > off ? SCRATCH_BYTES - off : 0;
     L.cap2 = tile_entries(ntiles, (T + 7) & ~7, left, 1);  // whole 64-byte lines per tile, as the fused kernel needs
+    if (L.segw && (size_t)seg_cap2 * ntiles * sizeof(drh::TileEnt) <= left)
+        L.cap2 = seg_cap2;
+    else
+        L.segw = 0;
     L.total = up(off + ntiles * (size_t)L.cap2 * sizeof(drh::TileEnt));
     return L;
 }
@@ -158,6 +168,7 @@ int drh_fused_loss_backward_noalloc(drh_ctx* ctx, const float* params, const flo
     bufs.tent = reinterpret_cast<drh::TileEnt*>(base + L.tent);
     bufs.cap2 = L.cap2;
     bufs.fused = fused_gradients(drh::MODE_LOSS, bufs.nseg, bufs.cap2, (int)T);
+    bufs.segw = bufs.fused ? L.segw : 0;
     // Nothing in the scratch array needs to start at zero: every buffer is
     // written by this call's kernels before it is read (the gradients are the
     // caller's output and setup_records clears them).

@@ -91,7 +91,10 @@ def test_fused_and_two_kernel_paths_agree(ctx, orc, name, B, H, W, T, sigma, kin
     # split backward and the rebuild past the recorded entries take. The loss
     # and image come from the same per-block sums (bit-equal); the gradients
     # differ only in the order of their float atomics, and not at all with
-    # fixed-order sums.
+    # fixed-order sums. On grids this small the default would take
+    # fused_seg_kernel (tests/test_gpu_segments.py), which composites in
+    # segments and rounds differently: DRH_NO_SEGMENTS=1 keeps the others.
+    monkeypatch.setenv("DRH_NO_SEGMENTS", "1")
     params, bgs = make_case(B, H, W, T, kind)
     targets = orc.render_batch(synth.batch(kind, B, T, 100, target_offset=1000), H, W, sigma, bgs[::-1].copy())
     gin = ((synth.uniforms(8, B * H * W * 3) - 0.5) * 1e-3).reshape(B, H, W, 3).astype(np.float32)
@@ -509,7 +512,13 @@ def test_random_shapes_match_oracle(ctx, orc, i, monkeypatch):
     dl, dg = ctx.fused_loss_backward(params, targets, sigma, bgs, deterministic=True)
     assert np.array_equal(dl, losses[False])
     assert_grads(dg, cg, label=f"case {i} fixed-order")
+    # the fused kernels other than fused_seg_kernel (which small grids take by
+    # default and which rounds its segment composite differently)
+    monkeypatch.setenv("DRH_NO_SEGMENTS", "1")
+    nl, ng = ctx.fused_loss_backward(params, targets, sigma, bgs)
+    check_losses(nl, cl, label=f"case {i} no segments")
+    assert_grads(ng, cg, label=f"case {i} no segments")
     monkeypatch.setenv("DRH_UNFUSED", "1")
     ul, ug = ctx.fused_loss_backward(params, targets, sigma, bgs)
-    assert np.array_equal(ul, losses[False])
+    assert np.array_equal(ul, nl)
     assert_grads(ug, cg, label=f"case {i} two kernels")

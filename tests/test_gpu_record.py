@@ -66,6 +66,15 @@ def both_paths(ctx, params, bgs, grad_images, H, W, sigma, flags=0, backwards=1)
             grads_a.cpu().numpy())
 
 
+@pytest.fixture(autouse=True)
+def _sequential_rows(monkeypatch):
+    # The recorded backward sums its fixed-order rows per 16x16 block, as the
+    # fused kernels other than fused_seg_kernel do (which small grids take by
+    # default, with rows per 8x8 tile): those are the path these tests compare
+    # it with bit for bit.
+    monkeypatch.setenv("DRH_NO_SEGMENTS", "1")
+
+
 def case(B, H, W, T, kind, seed):
     params = synth.batch(kind, B, T, seed)
     bgs = synth.uniforms(seed + 7, B * 3).reshape(B, 3).astype(np.float32)
@@ -79,12 +88,18 @@ def case(B, H, W, T, kind, seed):
     (2, 37, 53, 200, 0.004, "small"),
     (1, 64, 64, 32, 0.02, "uniform"),
 ])
-def test_record_path_equals_the_render_and_rerender_path(ctx, orc, B, H, W, T, sigma, kind, exact):
+def test_record_path_equals_the_render_and_rerender_path(ctx, orc, B, H, W, T, sigma, kind, exact, monkeypatch):
     params, bgs, gi = case(B, H, W, T, kind, 40 + T)
     flags = _lib.DETERMINISTIC | (_lib.EXACT_MATH if exact else 0)
+    # bit-equal to the other fused kernels (the fixture), and to
+    # fused_seg_kernel up to the association of its per-tile rows
+    monkeypatch.delenv("DRH_NO_SEGMENTS")
+    img_s, _, _, g_s = both_paths(ctx, params, bgs, gi, H, W, sigma, flags)
+    monkeypatch.setenv("DRH_NO_SEGMENTS", "1")
     img_r, (g_r,), img_a, g_a = both_paths(ctx, params, bgs, gi, H, W, sigma, flags)
-    assert np.array_equal(img_r, img_a)
+    assert np.array_equal(img_r, img_a) and np.array_equal(img_s, img_r)
     assert np.array_equal(g_r, g_a)
+    assert grad_err(g_s, g_r) <= 1e-6
     assert np.abs(img_r - orc.render_batch(params, H, W, sigma, bgs)).max() <= IMG_TOL
     assert grad_err(g_r, orc.backward_from_grad_batch(params, gi, sigma, bgs)) <= GRAD_RTOL
 
