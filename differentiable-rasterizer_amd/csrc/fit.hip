@@ -1,13 +1,15 @@
 // The fit loop (crates/diffrast/src/fit.rs:166-335) behind the C ABI: a
 // step-wise fitter whose state lives on the device, and drh_fit on top of it.
 //
-// Every iteration is setup_records -> the deterministic raster kernels ->
-// fit_step, which sums the partial rows in a fixed order (so a fit with a
-// given start is reproducible like the reference's, fit.rs:487-496) and does
-// the bookkeeping of fit.rs:243-288 on the device: divergence stop before the
-// optimizer sees the loss, loss record, best snapshot taken before the update,
-// patience, then Adam and the projection. The device state is double-buffered
-// by iteration parity (iteration i reads state i & 1 and writes the other).
+// Every iteration is the deterministic raster kernels -> fit_step, which sums
+// the partial rows in a fixed order (so a fit with a given start is
+// reproducible like the reference's, fit.rs:487-496) and does the bookkeeping
+// of fit.rs:243-288 on the device: divergence stop before the optimizer sees
+// the loss, loss record, best snapshot taken before the update, patience, then
+// Adam and the projection, and makes the next iteration's triangle records
+// (the first iteration's come from setup_records). The device state is
+// double-buffered by iteration parity (iteration i reads state i & 1 and
+// writes the other).
 // Once fit_step has stopped the fit, every kernel of a later iteration returns
 // at entry (the `halt` flag mirrors the stop code) and fit_step only carries
 // the state forward, so iterations launched ahead of a host check do no work.
@@ -31,12 +33,14 @@ struct drh_fitter {
     uint32_t math = 0;  // DRH_EXACT_MATH or 0
     int T = 0, H = 0, W = 0;
     drh_fit_config cfg{};
-    Lease work, state, images;
+    Lease work, state, images, recs;
     // work: params, m, v, lr, grads, best (T x 10 each), losses (iters), loss (1)
     float *params = nullptr, *m = nullptr, *v = nullptr, *lr = nullptr, *grads = nullptr, *best = nullptr;
     float *losses = nullptr, *loss = nullptr;
     // images: the target (H x W x 3) and the background (3)
     float *target = nullptr, *bg = nullptr;
+    float* rec = nullptr;         // the triangle records (T x REC; null when T = 0)
+    int64_t rec_iter = -1;        // the iteration whose records `rec` holds (fit_step makes the next one's)
     drh::FitState* st = nullptr;  // two states, by iteration parity
     int* halt = nullptr;          // the stop code once stopped, else -1
     drh::FitState last{};   // the device state as last read back
@@ -88,9 +92,17 @@ int launch_iteration(drh_fitter* f, int64_t i) {
     tail.halt = f->halt;
     tail.losses_out = f->losses;
     tail.best = f->best;
+    // the records: made by the previous iteration's fit_step when that was i - 1
+    tail.rec = f->rec;
+    tail.rec_ready = f->rec && f->rec_iter == i ? 1 : 0;
+    tail.sigma_next = sigma_at(f->cfg, i + 1);
+    tail.W = f->W;
+    tail.H = f->H;
+    f->rec_iter = -1;
     int rc = run_raster(f->ctx, drh::MODE_LOSS, f->params, f->bg, f->target, 1, f->T, f->H, f->W, sigma, nullptr,
                         f->grads, f->loss, flags, f->s, f->halt, &tail);
     if (rc) return rc;
+    f->rec_iter = f->rec ? i + 1 : -1;
     f->launched = i + 1;
     return DRH_OK;
 }
@@ -172,6 +184,8 @@ int drh_fitter_create(drh_ctx* ctx, const float* target, int64_t H, int64_t W, c
     if ((rc = f->work.acquire(ctx, K_FIT_F32, (n * 6 + iters + 1) * sizeof(float), f->s))) return bail(rc);
     if ((rc = f->state.acquire(ctx, K_FIT_STATE, sizeof(FitDevState), f->s))) return bail(rc);
     if ((rc = f->images.acquire(ctx, K_FIT_TARGET, (npix3 + 3) * sizeof(float), f->s))) return bail(rc);
+    if ((rc = f->recs.acquire(ctx, K_REC, (size_t)T * drh::REC * sizeof(float), f->s))) return bail(rc);
+    f->rec = f->recs.get<float>();
     f->params = f->work.get<float>();
     f->m = f->params + n;
     f->v = f->m + n;

@@ -60,8 +60,10 @@ enum : int { SETUP_RENDER = 0, SETUP_TAPE = 1, SETUP_RECORD = 2 };
 constexpr int CAP2_MIN = 128;
 
 // fused_seg_kernel: waves per tile, and the most triangles per scene (its LDS
-// holds a 288-byte record per entry of the tile: 46 KB at 160).
-constexpr int SEG_WAVES = 4;
+// holds a 288-byte record per entry slot of the tile, SEG_WAVES x a multiple of
+// 8 slots: 55 KB at 160). Eight waves measured faster than four (B=1 64x64
+// T=32: 18.0 -> 15.3 us; the 176x176 T=150 fit: 26.4 -> 23.4 us per iteration).
+constexpr int SEG_WAVES = 8;
 constexpr int SEG_MAX_T = 160;
 
 // One recorded entry of a tile's list, written by the forward kernel and read
@@ -207,7 +209,19 @@ struct FitTail {
     FitState* st;  // 2 states
     int* halt;
     float *losses_out, *best;
+    // The fit's triangle records, or null (pooled per call). rec_ready: they
+    // already hold this iteration's (the previous fit_step made them), so
+    // setup_records is not launched. fit_step makes the next iteration's, at
+    // sigma_next on the W x H canvas, from its updated parameters: a fit
+    // iteration is then two kernels.
+    float* rec;
+    int rec_ready;
+    float sigma_next;
+    int W, H;
 };
+// fit_step's parameter columns per block: whole triangles, so that a block
+// can make its triangles' records once it has updated them.
+constexpr int FIT_TRIS = 6;
 
 dim3 raster_grid(int B, int W, int H);
 // nblk partial rows (and loss partials) per scene, loss_per of which form a

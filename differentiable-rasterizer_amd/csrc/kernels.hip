@@ -2160,12 +2160,13 @@ __global__ void adam_project(float* __restrict__ params, const float* __restrict
 // The fit loop's iteration tail in one kernel (B = 1): reduce_partials' sums,
 // then the iteration's bookkeeping (fit.rs:243-288: divergence, loss record,
 // best, patience), the best snapshot before the update, and Adam
-// (optim.rs:40-60) with the projection (fit.rs:399-424), for the parameter
-// columns [64 x, 64 x + 64) of block x. Every block sums the loss
-// partials in reduce_partials' order and decides from st[iter & 1], so all
-// take the same decision; block 0 records it in st[(iter + 1) & 1] (and the
-// loss, the loss history and `halt`). An iteration launched after the stop
-// only carries the state forward (its raster kernels returned at entry).
+// (optim.rs:40-60) with the projection (fit.rs:399-424), for the parameters
+// of triangles [FIT_TRIS x, FIT_TRIS x + FIT_TRIS) of block x; with ft.rec,
+// then those triangles' records for the next iteration. Every block sums the
+// loss partials in reduce_partials' order and decides from st[iter & 1], so
+// all take the same decision; block 0 records it in st[(iter + 1) & 1] (and
+// the loss, the loss history and `halt`). An iteration launched after the
+// stop only carries the state forward (its raster kernels returned at entry).
 __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restrict__ partials,
                                                            const double* __restrict__ partial_loss, int nblk,
                                                            int loss_per, int T, double npix3, FitTail ft) {
@@ -2181,18 +2182,20 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = T * NP;
-    const int col = blockIdx.x * 64 + lane;
+    // FIT_TRIS whole triangles per block (lanes 60-63 idle)
+    const int col = blockIdx.x * (FIT_TRIS * NP) + lane;
+    const bool mine = lane < FIT_TRIS * NP && col < cols;
     // Wave 0's Adam operands, loaded here so that they arrive with the sums
     // (only this thread writes column col in this kernel).
     float p0 = 0.0f, m0 = 0.0f, v0 = 0.0f, lr0 = 0.0f;
-    if (wave == 0 && col < cols) {
+    if (wave == 0 && mine) {
         p0 = ft.params[col];
         m0 = ft.m[col];
         v0 = ft.v[col];
         lr0 = ft.lr[col];
     }
     float acc = 0.0f;
-    if (col < cols)
+    if (mine)
         acc = sum_rows_in_order(partials + col, cols, (nblk * wave) / RED_WAVES, (nblk * (wave + 1)) / RED_WAVES);
     part[wave][lane] = acc;
     if (wave == 1) {
@@ -2229,7 +2232,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
     }
     __syncthreads();
     const int d = decision;
-    if (wave == 0 && col < cols) {
+    if (wave == 0 && mine) {
         float g = part[0][lane];
         for (int q = 1; q < RED_WAVES; q++) g += part[q][lane];
         ft.grads[col] = g;
@@ -2249,6 +2252,14 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
                 ft.params[col] = pv;
             }
         }
+    }
+    if (ft.rec) {
+        // the next iteration's records of the block's triangles, as
+        // setup_records would make them from the updated parameters
+        __syncthreads();
+        const int k = blockIdx.x * FIT_TRIS + (int)threadIdx.x;
+        if ((int)threadIdx.x < FIT_TRIS && k < T)
+            setup_one(ft.params, (size_t)k, ft.W, ft.H, ft.sigma_next, SETUP_TAPE, ft.rec, nullptr);
     }
 }
 
@@ -2314,7 +2325,7 @@ hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const Sr
 hipError_t launch_fit_step(const float* partials, const double* partial_loss, int nblk, int loss_per, int T,
                            double npix3, const FitTail& ft, hipStream_t s) {
     if (loss_per != 1 && (loss_per != WAVES || nblk % WAVES != 0)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((T * NP + 63) / 64));
+    const dim3 grid((unsigned)((T + FIT_TRIS - 1) / FIT_TRIS));
     hipLaunchKernelGGL(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T, npix3, ft);
     return hipGetLastError();
 }

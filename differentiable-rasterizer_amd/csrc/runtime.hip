@@ -318,7 +318,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     if (bufs.order)
         ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3, bufs.rows, bufs.row_n}
                                : drh::OrderArgs{bufs.order, (int)grid.x, (int)grid.y, 4};
-    {
+    if (!(tail && tail->rec_ready)) {  // else the previous fit_step made this iteration's records
         KernelTimer kt(ctx, TK_SETUP, s, timed);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
                                   mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, bufs.rec,
@@ -407,7 +407,8 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     RasterBufs bufs;
     // whole 64-byte lines per tile (8 entries), as the fused kernel needs
     bufs.cap2 = tile_entries(ntiles, (T + 7) & ~7);
-    int rc = rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
+    // the records: the fit's own (FitTail::rec), else pooled
+    int rc = tail && tail->rec ? DRH_OK : rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
     const bool ordered =
         use_order(ctx, B, (int)grid.x, (int)grid.y) && (mode != drh::MODE_RENDER || T <= FWD_ORDER_MAX_T);
@@ -459,7 +460,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
             if ((rc = tn.acquire(ctx, K_TILE_N, ntiles * 2 * sizeof(int), s))) return rc;
         }
     }
-    bufs.rec = rec.get<float>();
+    bufs.rec = tail && tail->rec ? tail->rec : rec.get<float>();
     bufs.partials = partials.get<float>();
     bufs.ploss = ploss.get<double>();
     bufs.pq = pq.get<float>();

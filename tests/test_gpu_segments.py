@@ -1,6 +1,6 @@
 """fused_seg_kernel: the gradient calls on grids of few tiles (a single scene of
 a few hundred 8x8 tiles, the fit), where each tile's triangles are split over
-four waves that evaluate their weights and sweep their gradients in parallel,
+eight waves that evaluate their weights and sweep their gradients in parallel,
 while the composite between them runs in scene order.
 
 Against the oracle at the usual bars (tests/bars.py); against the other fused
@@ -19,11 +19,11 @@ from diffrast import synth
 pytestmark = pytest.mark.gpu
 
 # (name, B, H, W, T, sigma, kind): every one within the segmented kernel's
-# share (at most 2048 tiles, 8 to 160 triangles)
+# share (at most 2048 tiles, 16 to 160 triangles)
 CASES = [
     ("64x64-T32", 1, 64, 64, 32, 0.0015, "uniform"),
     ("fit-176-T150", 1, 176, 176, 150, 0.02, "uniform"),
-    ("odd-T13", 3, 37, 45, 13, 0.01, "uniform"),
+    ("odd-T19", 3, 37, 45, 19, 0.01, "uniform"),
     ("small-T144", 2, 64, 96, 144, 0.004, "small"),
     ("tiny-sigma", 2, 32, 32, 24, 1e-4, "uniform"),
     ("T160", 1, 40, 56, 160, 0.006, "small"),
