@@ -60,9 +60,9 @@ enum : int { SETUP_RENDER = 0, SETUP_TAPE = 1, SETUP_RECORD = 2 };
 constexpr int CAP2_MIN = 128;
 
 // fused_seg_kernel: waves per tile, and the most triangles per scene (its LDS
-// holds a 288-byte record per entry slot of the tile, SEG_WAVES x a multiple of
-// 8 slots: 55 KB at 160). Eight waves measured faster than four (B=1 64x64
-// T=32: 18.0 -> 15.3 us; the 176x176 T=150 fit: 26.4 -> 23.4 us per iteration).
+// holds a 288-byte record per triangle of the scene, 45 KB at 160). Eight
+// waves measured faster than four (B=1 64x64 T=32: 18.0 -> 15.3 us; the
+// 176x176 T=150 fit: 26.4 -> 23.4 us per iteration).
 constexpr int SEG_WAVES = 8;
 constexpr int SEG_MAX_T = 160;
 
@@ -222,6 +222,16 @@ struct FitTail {
 // fit_step's parameter columns per block: whole triangles, so that a block
 // can make its triangles' records once it has updated them.
 constexpr int FIT_TRIS = 6;
+
+// Events that the calling thread's next kernel launch in this library takes
+// as its start and stop (hipExtLaunchKernel: the kernel's own start and end,
+// with no event packets of their own around it), or null; `used` is set by the
+// launch. The runtime's per-kernel timing (drh_timing_enable) sets them.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool used = false;
+};
+LaunchEvents& launch_events();
 
 dim3 raster_grid(int B, int W, int H);
 // nblk partial rows (and loss partials) per scene, loss_per of which form a

@@ -31,6 +31,7 @@
 // appear only where the reference's rounding cannot change a result beyond
 // the stated tolerance (gradient assembly, conservative classification).
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <climits>
 #include <stdint.h>
@@ -39,6 +40,24 @@
 #include "kernels.h"
 
 namespace drh {
+
+namespace {
+thread_local LaunchEvents t_launch_events;
+}  // namespace
+LaunchEvents& launch_events() { return t_launch_events; }
+
+// Every launch of this file: hipExtLaunchKernel, with the calling thread's
+// timing events when it has some (launch_events), which then go to this
+// launch alone.
+template <typename F, typename... Args>
+static void launch_k(F kernel, const dim3& grid, const dim3& block, size_t lds, hipStream_t s, Args... args) {
+    LaunchEvents& ev = t_launch_events;
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, ev.start, ev.stop, 0u, args...);
+    if (ev.start) {
+        ev.used = true;
+        ev.start = ev.stop = nullptr;
+    }
+}
 
 constexpr float MIN_WEIGHT = 1e-6f;  // raster.rs:31-34
 
@@ -1843,8 +1862,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
 // summed four to a 16x16 block first, as sum_losses sums the one-wave
 // kernel's.
 //
-// Dynamic LDS: phases A and B hold cap2 SegEnt records; phase C reuses the
-// same area for the waves' transposition areas (and DET accumulator rows).
+// Dynamic LDS: phases A and B hold SEG_WAVES x seg_tris(T) SegEnt records;
+// phase C reuses the same area for the waves' transposition areas (and DET
+// accumulator rows).
 struct SegEnt {
     float w[64];       // weight at each lane's pixel
     float c[3];        // colour
@@ -1854,13 +1874,17 @@ struct SegEnt {
 static_assert(sizeof(SegEnt) == 288 && sizeof(SegEnt) % 16 == 0, "SegEnt keeps 16-byte alignment");
 constexpr int SEG_MAX = SEG_MAX_T / SEG_WAVES;  // triangles per segment
 
-// Phase C's LDS bytes, and the workgroup's dynamic LDS.
-__host__ __device__ constexpr size_t seg_lds_c(bool det, int cap_s) {
-    return (size_t)SEG_WAVES * NP * TP * sizeof(float) + (det ? (size_t)SEG_WAVES * cap_s * NP * sizeof(float) : 0);
+// Triangles per segment (at most), the pitch of the segments' SegEnt records
+// in LDS; phase C's LDS bytes; and the workgroup's dynamic LDS.
+__host__ __device__ constexpr int seg_tris(int T) { return (T + SEG_WAVES - 1) / SEG_WAVES; }
+__host__ __device__ constexpr size_t seg_lds_c(bool det, int T) {
+    return (size_t)SEG_WAVES * NP * TP * sizeof(float) +
+           (det ? (size_t)SEG_WAVES * seg_tris(T) * NP * sizeof(float) : 0);
 }
-__host__ __device__ constexpr size_t seg_lds_bytes(bool det, int cap2) {
-    return (size_t)cap2 * sizeof(SegEnt) > seg_lds_c(det, cap2 / SEG_WAVES) ? (size_t)cap2 * sizeof(SegEnt)
-                                                                              : seg_lds_c(det, cap2 / SEG_WAVES);
+__host__ __device__ constexpr size_t seg_lds_bytes(bool det, int T) {
+    return (size_t)SEG_WAVES * seg_tris(T) * sizeof(SegEnt) > seg_lds_c(det, T)
+               ? (size_t)SEG_WAVES * seg_tris(T) * sizeof(SegEnt)
+               : seg_lds_c(det, T);
 }
 
 template <int MODE, bool FAST, bool DET, int S>
@@ -1882,7 +1906,8 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
     const float rsig = a.rsig;
     const float* __restrict__ rec = records + (size_t)b * T * REC;
     const int k0 = (int)(((long long)s * T) / S), k1 = (int)(((long long)(s + 1) * T) / S);
-    const int capS = a.cap2 / S;
+    const int capS = a.cap2 / S;     // entry slots per segment in the tile's region
+    const int lcap = seg_tris(T);    // SegEnt slots per segment in LDS (>= k1 - k0)
     // wave-uniform: the entry stores and loads address from a scalar base
     TileEnt* const te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * a.cap2 + s * capS;
 
@@ -1908,7 +1933,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             Geo g;
             const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
             if (onm == 0) continue;  // wave-uniform
-            SegEnt& e = sent[s * capS + n2];
+            SegEnt& e = sent[s * lcap + n2];
             e.w[lane] = w;
             if (lane == 0) {
                 e.c[0] = r.f(R_C);
@@ -1945,7 +1970,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
         }
         const int n = nent[q];
         for (int i = 0; i < n; i++) {
-            const SegEnt& e = sent[q * capS + i];
+            const SegEnt& e = sent[q * lcap + i];
             const float w = e.w[lane];
             const bool on = ((lane < 32 ? e.on[0] >> lane : e.on[1] >> (lane - 32)) & 1u) != 0;
             const float omw = 1.0f - w;
@@ -1989,9 +2014,9 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
 
     // C. this segment's entries backward
     lds_float* const tw = (lds_float*)(seg_lds + s * (NP * TP));
-    lds_float* const accs = (lds_float*)(seg_lds + S * (NP * TP) + s * (capS * NP));
+    lds_float* const accs = (lds_float*)(seg_lds + S * (NP * TP) + s * (lcap * NP));
     if (DET) {
-        for (int j = lane; j < capS * NP; j += 64) accs[j] = 0.0f;
+        for (int j = lane; j < lcap * NP; j += 64) accs[j] = 0.0f;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -2310,13 +2335,13 @@ static dim3 stream_grid(int64_t n) {
 
 hipError_t launch_encode_srgb(const float* in, int64_t n, uint8_t* out, const SrgbTable& thresholds, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(encode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, thresholds);
+    launch_k(encode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, thresholds);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_srgb(const uint8_t* in, int64_t n, float* out, const SrgbTable& values, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(decode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, values);
+    launch_k(decode_srgb_kernel, stream_grid(n), dim3(256), 0, s, in, n, out, values);
     return hipGetLastError();
 }
 
@@ -2326,7 +2351,7 @@ hipError_t launch_fit_step(const float* partials, const double* partial_loss, in
                            double npix3, const FitTail& ft, hipStream_t s) {
     if (loss_per != 1 && (loss_per != WAVES || nblk % WAVES != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((T + FIT_TRIS - 1) / FIT_TRIS));
-    hipLaunchKernelGGL(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T, npix3, ft);
+    launch_k(fit_step, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T, npix3, ft);
     return hipGetLastError();
 }
 
@@ -2346,7 +2371,7 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     oa.w_cells = (float)W / cs;
     oa.c0_off = (0.5f - cs) / cs;
     oa.c1_off = -0.5f / cs;
-    hipLaunchKernelGGL(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
+    launch_k(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
                        zero_grads, bg_src, bg_dst, oa, halt, head, head_val);
     return hipGetLastError();
 }
@@ -2354,7 +2379,7 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
 hipError_t launch_zero(float* p, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     const size_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(zero_floats, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, p, n);
+    launch_k(zero_floats, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 
@@ -2364,7 +2389,7 @@ dim3 raster_grid(int B, int W, int H) {
 
 template <int MODE, bool FAST, bool CKPT = false>
 static hipError_t launch_forward_t(const RasterArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((forward_kernel<MODE, FAST, CKPT>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a,
+    launch_k((forward_kernel<MODE, FAST, CKPT>), raster_grid(a.B, a.W, a.H), dim3(WAVES * 64), 0, s, a,
                        a.rec);
     return hipGetLastError();
 }
@@ -2388,7 +2413,7 @@ template <int MODE, bool FAST, bool REBUILD, bool DET>
 static hipError_t launch_backward_t(const RasterArgs& a, hipStream_t s) {
     const bool split = !REBUILD && !DET && a.perm_bwd && a.nseg > 1;
     const dim3 grid = split ? dim3((unsigned)(a.B * (a.gx * a.gy + a.nsplit * (a.nseg - 1)))) : raster_grid(a.B, a.W, a.H);
-    hipLaunchKernelGGL((backward_kernel<MODE, FAST, REBUILD, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+    launch_k((backward_kernel<MODE, FAST, REBUILD, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
     return hipGetLastError();
 }
 
@@ -2414,24 +2439,24 @@ hipError_t launch_backward(int mode, bool fast, bool rebuild, const RasterArgs& 
 template <int MODE, bool DET>
 static void launch_fused_d(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
     if (fast)
-        hipLaunchKernelGGL((fused_kernel<MODE, true, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_kernel<MODE, true, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
     else
-        hipLaunchKernelGGL((fused_kernel<MODE, false, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_kernel<MODE, false, DET>), grid, dim3(WAVES * 64), 0, s, a, a.rec, a.tl_ent);
 }
 
 template <int MODE>
 static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
     if (a.segw) {
         const dim3 tiles(grid.x * grid.y * grid.z * WAVES), threads(SEG_WAVES * 64);
-        const size_t lds = seg_lds_bytes(a.deterministic != 0, a.cap2);
+        const size_t lds = seg_lds_bytes(a.deterministic != 0, a.T);
         if (a.deterministic && fast)
-            hipLaunchKernelGGL((fused_seg_kernel<MODE, true, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+            launch_k((fused_seg_kernel<MODE, true, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
         else if (a.deterministic)
-            hipLaunchKernelGGL((fused_seg_kernel<MODE, false, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+            launch_k((fused_seg_kernel<MODE, false, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
         else if (fast)
-            hipLaunchKernelGGL((fused_seg_kernel<MODE, true, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+            launch_k((fused_seg_kernel<MODE, true, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
         else
-            hipLaunchKernelGGL((fused_seg_kernel<MODE, false, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
+            launch_k((fused_seg_kernel<MODE, false, false, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
         return;
     }
     if (a.deterministic) {
@@ -2441,13 +2466,13 @@ static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_
     const dim3 tiles(grid.x * grid.y * grid.z * WAVES);
     const bool rows = a.rows && a.row_n;
     if (fast && rows)
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
     else if (fast)
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, true, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, true, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
     else if (rows)
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, false, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, false, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
     else
-        hipLaunchKernelGGL((fused_tile_kernel<MODE, false, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, false, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
 }
 
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
@@ -2470,9 +2495,9 @@ hipError_t launch_sum_losses(const double* partial_loss, int B, int nblk, int pe
     if (B == 0) return hipSuccess;
     if (nblk <= 0) return hipErrorInvalidValue;
     if (per == WAVES)
-        hipLaunchKernelGGL(sum_losses<WAVES>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+        launch_k(sum_losses<WAVES>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
     else if (per == 1)
-        hipLaunchKernelGGL(sum_losses<1>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
+        launch_k(sum_losses<1>, dim3(B), dim3(64), 0, s, partial_loss, nblk, npix3, losses, halt);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2483,7 +2508,7 @@ hipError_t launch_reduce(const float* partials, const double* partial_loss, int 
     if (loss_per != 1 && (loss_per != WAVES || nblk % WAVES != 0)) return hipErrorInvalidValue;
     int cols = T * NP;
     dim3 grid((cols + 63) / 64 > 0 ? (cols + 63) / 64 : 1, B);
-    hipLaunchKernelGGL(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T,
+    launch_k(reduce_partials, grid, dim3(RED_WAVES * 64), 0, s, partials, partial_loss, nblk, loss_per, T,
                        npix3, grads, losses, halt);
     return hipGetLastError();
 }
@@ -2492,7 +2517,7 @@ hipError_t launch_adam(float* params, const float* grads, float* m, float* v, co
                        float beta1, float beta2, float eps, float bc1, float bc2, int project,
                        hipStream_t s) {
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(adam_project, dim3((n + 255) / 256), dim3(256), 0, s, params, grads, m, v, lr, n, beta1,
+    launch_k(adam_project, dim3((n + 255) / 256), dim3(256), 0, s, params, grads, m, v, lr, n, beta1,
                        beta2, eps, bc1, bc2, project);
     return hipGetLastError();
 }

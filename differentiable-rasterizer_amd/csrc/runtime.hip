@@ -251,13 +251,26 @@ float powi_f32(float a, int32_t b) {
 KernelTimer::KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s, bool enabled) : ctx_(ctx), s_(s) {
     if (!enabled || !ctx->timing) return;
     l_.kernel = kernel;
-    if (hipEventCreate(&l_.start) != hipSuccess || hipEventCreate(&l_.stop) != hipSuccess) return;
-    on_ = hipEventRecord(l_.start, s) == hipSuccess;
+    if (hipEventCreate(&l_.start) != hipSuccess) return;
+    if (hipEventCreate(&l_.stop) != hipSuccess) {
+        (void)hipEventDestroy(l_.start);
+        return;
+    }
+    // the scope's launch takes them as its own start and end (hipExtLaunchKernel)
+    drh::launch_events() = drh::LaunchEvents{l_.start, l_.stop, false};
+    on_ = true;
 }
 
 KernelTimer::~KernelTimer() {
     if (!on_) return;
-    (void)hipEventRecord(l_.stop, s_);
+    drh::LaunchEvents& ev = drh::launch_events();
+    const bool used = ev.used;
+    ev = drh::LaunchEvents{};
+    if (!used) {  // nothing was launched in the scope
+        (void)hipEventDestroy(l_.start);
+        (void)hipEventDestroy(l_.stop);
+        return;
+    }
     std::lock_guard<std::mutex> g(ctx_->mu);
     ctx_->pending.push_back(l_);
 }
