@@ -113,6 +113,17 @@ def time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev):
     return ms, losses, grads
 
 
+def fused_kernel_name(B, H, W, T, deterministic=False):
+    """The kernel the library's fused gradient path takes for this shape: the
+    segmented kernel for grids of at most 2048 8x8 tiles with 16 to 160
+    triangles (runtime.h: use_segments), else the one-wave tile kernel (the
+    four-wave block kernel with fixed-order sums)."""
+    tiles = B * ((W + 15) // 16) * ((H + 15) // 16) * 4
+    if 16 <= T <= 160 and tiles <= 2048:
+        return "fused_seg_kernel" + (" (fixed order)" if deterministic else "")
+    return "fused_kernel (fixed order)" if deterministic else "fused_tile_kernel"
+
+
 def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev, two_kernels=False):
     """Event-timed average duration of each kernel of the step: setup_records, then
     either fused_kernel and sum_losses, or (two_kernels: DRH_UNFUSED=1, and the
@@ -251,8 +262,8 @@ def fit_cpu(out, keep):
     out["speedup_gpu_over_cpu"] = cpu_s / dt
     flop = (FLOP_FWD[0] + FLOP_BWD[0]) * counts.n_box + (FLOP_FWD[1] + FLOP_BWD[1]) * counts.n_contrib \
         + FLOP_FWD[2] * iters * H * W
-    out["roofline"] = roof("fused_kernel (fixed order)", flop / iters, kt["fused"],
-                           traffic_from_profiles("fused_kernel", "c4"))
+    kname = fused_kernel_name(1, H, W, T, deterministic=True)
+    out["roofline"] = roof(kname, flop / iters, kt["fused"], traffic_from_profiles(kname.split(" ")[0], "c4"))
     out["roofline"]["n_box_pairs_all_iterations"] = int(counts.n_box)
     out["roofline"]["n_contrib_pairs_all_iterations"] = int(counts.n_contrib)
     out["roofline_step"] = roof("whole iteration (wall)", flop / iters, dt * 1e3 / iters)
@@ -475,8 +486,9 @@ def cpu_leg(out, keep, cpu_budget, traffic=True):
                                       k["forward"] + k["backward"])}
 
     if "fused" in kt:
-        out["roofline"] = roof("fused_tile_kernel", flop_f + flop_b, kt["fused"],
-                               traffic_from_profiles("fused_tile_kernel", name) if traffic else None)
+        kname = fused_kernel_name(B, H, W, T)
+        out["roofline"] = roof(kname, flop_f + flop_b, kt["fused"],
+                               traffic_from_profiles(kname, name) if traffic else None)
         if two is not None:
             two.update(two_kernel_roofs(two["kernel_ms"]))
             two["kernel_ms"] = {k: round(v, 5) for k, v in two["kernel_ms"].items()}
