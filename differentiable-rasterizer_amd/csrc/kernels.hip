@@ -329,9 +329,23 @@ __device__ inline void setup_one(const float* __restrict__ params, size_t i, int
 // heaviest first, and writes their scene-local indices to perm[b * nb ...]. The raster kernels take launch
 // slot i to rank i / B of scene i % B, so the heaviest blocks of every scene go
 // first. Nothing crosses workgroups: a device-wide hand-off would cost more
-// than the order saves.
-constexpr int SETUP_THREADS = 1024, ORD_BUCKETS = 1024, ORD_REACH = 256;
-static_assert(ORD_BUCKETS % SETUP_THREADS == 0 && SETUP_THREADS % 64 == 0, "order workgroup shape");
+// than the order saves. The records then come from workgroups of
+// SETUP_REC_PER triangles: a wave stores each record as 19 16-byte pieces at a
+// 304-byte stride, a cache line per lane and store, and one CU issues about one
+// line per cycle, so 512 records on one CU took ~6 us and on four ~1.5.
+constexpr int SETUP_THREADS = 1024, ORD_BUCKETS = 1024, ORD_REACH = 512, SETUP_REC_PER = 128;
+static_assert(ORD_BUCKETS == 16 * 64 && SETUP_THREADS % 64 == 0 && ORD_REACH <= SETUP_THREADS,
+              "order workgroup shape: 16 buckets per lane of one wave");
+
+// Inclusive prefix sum within each row of 16 lanes (every lane active): DPP
+// row shifts (lanes with no source read the `old` operand, 0).
+__device__ inline int row_scan_incl(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    return v;
+}
 
 // Inclusive prefix sum over the wave's lanes (every lane active).
 // DPP row shifts within each row of 16 lanes (lanes with no source read the
@@ -347,43 +361,49 @@ __device__ inline int wave_scan_incl(int v, int) {
     return v;
 }
 
-__device__ inline void order_scene(const OrderArgs& o, int* cells, int b, int T) {
-    static_assert(ORD_BUCKETS == SETUP_THREADS && SETUP_THREADS / 64 <= 64, "one bucket per thread");
-    __shared__ int hist[ORD_BUCKETS];
-    __shared__ int wsum[SETUP_THREADS / 64];
+// hist: ORD_BUCKETS zeroes (cleared before the caller's first barrier).
+__device__ inline void order_scene(const OrderArgs& o, int* cells, int* hist, int b, int T) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gx = o.gx, gy = o.gy, pitch = gx + 1, nb = gx * gy;
+    const int base = 6 * ((T + 63) / 64);  // list building, against one reaching triangle
+    auto key_of = [&](int count) { return ORD_BUCKETS - 1 - min(count + base, ORD_BUCKETS - 1); };
     // prefix sums along the cell rows, one wave per row at a time: 64 cells per
-    // step, a wave scan plus the carry of the row's earlier cells
+    // step, a wave scan plus the carry of the row's earlier cells; each cell's
+    // count goes into the histogram as soon as it is known
     for (int y = wave; y < gy; y += SETUP_THREADS / 64) {
         int carry = 0;
         for (int x0 = 0; x0 <= gx; x0 += 64) {
             const int x = x0 + lane;
             const int v = wave_scan_incl(x <= gx ? cells[y * pitch + x] : 0, lane);
             if (x <= gx) cells[y * pitch + x] = v + carry;
+            if (x < gx) atomicAdd(&hist[key_of(v + carry)], 1);
             carry += __shfl(v, 63, 64);
         }
     }
-    hist[t] = 0;
     __syncthreads();
-    const int base = 6 * ((T + 63) / 64);  // list building, against one reaching triangle
-    auto key = [&](int blk) {
-        const int c = cells[(blk / gx) * pitch + blk % gx] + base;
-        return ORD_BUCKETS - 1 - min(c, ORD_BUCKETS - 1);
-    };
-    for (int blk = t; blk < nb; blk += SETUP_THREADS) atomicAdd(&hist[key(blk)], 1);
-    __syncthreads();
-    // exclusive prefix of the histogram: a scan in each wave, then of the
-    // waves' totals
-    const int own = hist[t], incl = wave_scan_incl(own, lane);
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
+    // exclusive prefix of the histogram in one wave: lane l sums buckets
+    // 16 l .. 16 l + 15, a wave scan places the lanes' runs
     if (wave == 0) {
-        const int w = wave_scan_incl(lane < SETUP_THREADS / 64 ? wsum[lane] : 0, lane);
-        if (lane < SETUP_THREADS / 64) wsum[lane] = w;
+        typedef int i4v __attribute__((ext_vector_type(4)));
+        i4v* const h4 = reinterpret_cast<i4v*>(hist + 16 * lane);
+        i4v q[4];
+        int sum = 0;
+        for (int j = 0; j < 4; j++) {
+            q[j] = h4[j];
+            sum += (q[j].x + q[j].y) + (q[j].z + q[j].w);
+        }
+        int run = wave_scan_incl(sum, lane) - sum;
+        for (int j = 0; j < 4; j++) {
+            i4v e;
+            e.x = run;
+            e.y = e.x + q[j].x;
+            e.z = e.y + q[j].y;
+            e.w = e.z + q[j].z;
+            run = e.w + q[j].w;
+            h4[j] = e;
+        }
     }
     __syncthreads();
-    hist[t] = incl - own + (wave > 0 ? wsum[wave - 1] : 0);
-    __syncthreads();
+    auto key = [&](int blk) { return key_of(cells[(blk / gx) * pitch + blk % gx]); };
     for (int blk = t; blk < nb; blk += SETUP_THREADS) {
         const int pos = atomicAdd(&hist[key(blk)], 1);  // < nb: the offsets partition [0, nb)
         if (pos < nb) o.perm[(size_t)b * nb + pos] = blk;
@@ -403,15 +423,17 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
                                                                const int* __restrict__ halt,
                                                                RecordHead* __restrict__ head, RecordHead head_val) {
     __shared__ int cells[ORD_MAX_CELLS];
+    __shared__ __attribute__((aligned(16))) int hist[ORD_BUCKETS];
     if (halt && *halt >= 0) return;
     const int b = blockIdx.y, pitch = o.gx + 1;
-    const int nrec = (T + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int per = o.perm ? SETUP_REC_PER : (int)blockDim.x;  // records per workgroup
+    const int nrec = (T + per - 1) / per;
     if (head && b == 0 && blockIdx.x == 0 && threadIdx.x == 0) *head = head_val;
     // A record kept for a later backward holds its own copy of the backgrounds.
     if (bg_dst && blockIdx.x == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
     if (!o.perm || (int)blockIdx.x < nrec) {
-        const int k = blockIdx.x * blockDim.x + threadIdx.x;
-        if (k < T) setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
+        const int k = blockIdx.x * per + threadIdx.x;
+        if ((int)threadIdx.x < per && k < T) setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
         return;
     }
     // Triangles in batches of up to ORD_REACH: each one's Reach made by one
@@ -433,6 +455,7 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
     };
     load_batch(0);
     for (int c = threadIdx.x; c < (o.gy + 1) * pitch; c += SETUP_THREADS) cells[c] = 0;
+    for (int c = threadIdx.x; c < ORD_BUCKETS; c += SETUP_THREADS) hist[c] = 0;
     for (int k0 = 0; k0 < T; k0 += ORD_REACH) {
         const int nt = min(ORD_REACH, T - k0);
         if ((int)threadIdx.x < nt) reach[threadIdx.x] = make_reach(pk, W, H, sigma, o.shift);
@@ -444,25 +467,42 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
             reach_rows(reach[w >> lg], o, w & (m - 1), m, cells, pitch, rowmask, words, k0 + (w >> lg));
         __syncthreads();
     }
-    if (rowmask) {
-        // each row's set bits in index order, one wave per row: a wave scan of
-        // the words' bit counts places each word's indices
-        const int lane = threadIdx.x & 63;
-        for (int y = threadIdx.x >> 6; y < o.gy; y += SETUP_THREADS / 64) {
-            int* out = o.rows + ((size_t)b * o.gy + y) * T;
-            int carry = 0;
-            for (int w0 = 0; w0 < words; w0 += 64) {
-                const int w = w0 + lane;
-                uint32_t bits = w < words ? rowmask[y * words + w] : 0u;
-                const int cnt = __popc(bits), incl = wave_scan_incl(cnt, lane);
-                int pos = carry + incl - cnt;
-                for (; bits; bits &= bits - 1) out[pos++] = 32 * w + __ffs((int)bits) - 1;
-                carry += __shfl(incl, 63, 64);
+    order_scene(o, cells, hist, b, T);
+    if (!rowmask) return;
+    // Each row's set bits in index order: a scan of the words' bit counts
+    // places each word's indices. Up to 16 words (512 triangles) a row takes
+    // one 16-lane row of a wave (four rows per wave, DPP row scans), so that
+    // every row is expanded in one pass instead of one row after another.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (words <= 16) {
+        const int sub = lane >> 4, wl = lane & 15;
+        for (int y0 = 4 * wave; y0 < o.gy; y0 += 4 * (SETUP_THREADS / 64)) {
+            const int y = y0 + sub;
+            uint32_t bits = y < o.gy && wl < words ? rowmask[y * words + wl] : 0u;
+            const int cnt = __popc(bits), incl = row_scan_incl(cnt);
+            const int total = __shfl(incl, lane | 15, 64);
+            if (y < o.gy) {
+                int* out = o.rows + ((size_t)b * o.gy + y) * T;
+                int pos = incl - cnt;
+                for (; bits; bits &= bits - 1) out[pos++] = 32 * wl + __ffs((int)bits) - 1;
+                if (wl == 0) o.row_n[(size_t)b * o.gy + y] = total;
             }
-            if (lane == 0) o.row_n[(size_t)b * o.gy + y] = carry;
         }
+        return;
     }
-    order_scene(o, cells, b, T);
+    for (int y = wave; y < o.gy; y += SETUP_THREADS / 64) {
+        int* out = o.rows + ((size_t)b * o.gy + y) * T;
+        int carry = 0;
+        for (int w0 = 0; w0 < words; w0 += 64) {
+            const int w = w0 + lane;
+            uint32_t bits = w < words ? rowmask[y * words + w] : 0u;
+            const int cnt = __popc(bits), incl = wave_scan_incl(cnt, lane);
+            int pos = carry + incl - cnt;
+            for (; bits; bits &= bits - 1) out[pos++] = 32 * w + __ffs((int)bits) - 1;
+            carry += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) o.row_n[(size_t)b * o.gy + y] = carry;
+    }
 }
 
 // ---------------------------------------------------------------- per-pair math
@@ -2363,7 +2403,8 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     // without an order, small workgroups spread the triangles over more CUs;
     // with one, a last workgroup per scene makes it
     const int n = o.perm ? SETUP_THREADS : 64;
-    const int gx = (T + n - 1) / n + (o.perm || T == 0 ? 1 : 0);
+    const int per = o.perm ? SETUP_REC_PER : n;  // records per workgroup (setup_records' `per`)
+    const int gx = (T + per - 1) / per + (o.perm || T == 0 ? 1 : 0);
     OrderArgs oa = o;
     const float cs = (float)(1 << o.shift);
     oa.r_h = 1.0f / (float)H;

@@ -10,8 +10,8 @@ gradient norm), and, with DRH_DETERMINISTIC, be bit-identical from call to call.
 cases are sized to take the ordered paths: 4 scenes of 160 x 200 px are 4 x 10 x 13 =
 520 blocks; 2 scenes of 720 x 768 px have 90 x 96 tiles each, past the tile order's
 8192 cells, so their one-wave fused kernel takes the block order; 2 scenes of 1100
-small triangles take the order workgroup's triangles in five batches of up to 256
-and the records in two workgroups of 1024. From 256 triangles on, the one-wave
+small triangles take the order workgroup's triangles in three batches of up to 512
+and the records in nine workgroups of 128. From 256 triangles on, the one-wave
 fused kernel's lists scan only the triangles of their tile row, which setup_records
 lists (the small-triangle cases, and 300 large triangles at 256 x 256).
 """
