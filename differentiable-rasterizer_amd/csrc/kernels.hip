@@ -410,11 +410,14 @@ __device__ inline void order_scene(const OrderArgs& o, int* cells, int* hist, in
     }
 }
 
-// Workgroup (x, b) with x < nrec = ceil(T / n), n the workgroup size: the
-// records of scene b's triangles [x n, x n + n). With o.perm (then
-// n == SETUP_THREADS), workgroup (nrec, b) makes the scene's block order from
-// the triangles' boxes, computed again from the parameters, concurrently with
-// the records.
+// Workgroup (b, y): the records of scene b's triangles [x per, x per + per)
+// (and every nx per after, nx the records workgroups per scene), per the
+// records per workgroup and x = y. With o.perm (then the workgroup
+// size is SETUP_THREADS and per SETUP_REC_PER), workgroup (b, 0) makes the
+// scene's block order from the triangles' boxes, computed again from the
+// parameters, concurrently with the records of workgroups (b, x + 1). The
+// order workgroups, the longest, come first in the grid, so that they are
+// dispatched before any records.
 __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __restrict__ params, int T, int W,
                                                                int H, float sigma, int setup_mode,
                                                                float* __restrict__ rec, float* __restrict__ zero_grads,
@@ -425,15 +428,17 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
     __shared__ int cells[ORD_MAX_CELLS];
     __shared__ __attribute__((aligned(16))) int hist[ORD_BUCKETS];
     if (halt && *halt >= 0) return;
-    const int b = blockIdx.y, pitch = o.gx + 1;
+    const int b = blockIdx.x, part = blockIdx.y, pitch = o.gx + 1;
     const int per = o.perm ? SETUP_REC_PER : (int)blockDim.x;  // records per workgroup
-    const int nrec = (T + per - 1) / per;
-    if (head && b == 0 && blockIdx.x == 0 && threadIdx.x == 0) *head = head_val;
+    if (head && b == 0 && part == 0 && threadIdx.x == 0) *head = head_val;
     // A record kept for a later backward holds its own copy of the backgrounds.
-    if (bg_dst && blockIdx.x == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
-    if (!o.perm || (int)blockIdx.x < nrec) {
-        const int k = blockIdx.x * per + threadIdx.x;
-        if ((int)threadIdx.x < per && k < T) setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
+    if (bg_dst && part == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
+    if (!o.perm || part > 0) {
+        // grid rows are capped at 65535: a records workgroup strides over the rest
+        const int nparts = (int)gridDim.y - (o.perm ? 1 : 0);
+        if ((int)threadIdx.x < per)
+            for (int k = (o.perm ? part - 1 : part) * per + (int)threadIdx.x; k < T; k += nparts * per)
+                setup_one(params, (size_t)b * T + k, W, H, sigma, setup_mode, rec, zero_grads);
         return;
     }
     // Triangles in batches of up to ORD_REACH: each one's Reach made by one
@@ -2404,7 +2409,7 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     // with one, a last workgroup per scene makes it
     const int n = o.perm ? SETUP_THREADS : 64;
     const int per = o.perm ? SETUP_REC_PER : n;  // records per workgroup (setup_records' `per`)
-    const int gx = (T + per - 1) / per + (o.perm || T == 0 ? 1 : 0);
+    const int gx = min((T + per - 1) / per, 65534) + (o.perm || T == 0 ? 1 : 0);
     OrderArgs oa = o;
     const float cs = (float)(1 << o.shift);
     oa.r_h = 1.0f / (float)H;
@@ -2412,7 +2417,7 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     oa.w_cells = (float)W / cs;
     oa.c0_off = (0.5f - cs) / cs;
     oa.c1_off = -0.5f / cs;
-    launch_k(setup_records, dim3(gx, B), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
+    launch_k(setup_records, dim3(B, gx), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
                        zero_grads, bg_src, bg_dst, oa, halt, head, head_val);
     return hipGetLastError();
 }
