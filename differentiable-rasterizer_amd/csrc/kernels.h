@@ -65,6 +65,11 @@ constexpr int CAP2_MIN = 128;
 // 176x176 T=150 fit: 26.4 -> 23.4 us per iteration).
 constexpr int SEG_WAVES = 8;
 constexpr int SEG_MAX_T = 160;
+// A loss slot not yet written (RasterArgs::loss_tail): a signalling NaN with
+// the lowest mantissa bit set. Arithmetic only returns quiet NaNs, and NaNs
+// that reach the loss from float inputs have their low 29 mantissa bits clear,
+// so no partial loss has these bits.
+constexpr uint64_t LOSS_PENDING = 0xFFF4C0DE5EED0001ull;
 
 // One recorded entry of a tile's list, written by the forward kernel and read
 // (with scalar loads) by the backward kernel.
@@ -136,6 +141,13 @@ struct RasterArgs {
     int* tl_n;             // ntiles*2: entries recorded, chunks fully recorded | TN_IRREGULAR
     float* grads;          // B*T*NP, accumulated with atomics unless deterministic
     float* losses;         // B (MODE_LOSS)
+    // MODE_LOSS, the fused kernels outside the fixed-order mode (one-wave and
+    // segmented): the grid's last B workgroups sum each
+    // scene's per-tile loss partials into `losses` (no sum_losses launch). The
+    // tiles store their partials with device-scope atomic stores into slots
+    // that setup_records filled with LOSS_PENDING, and each summing workgroup
+    // polls its scene's slots (device-scope atomic loads) until none is pending.
+    int loss_tail;
     int deterministic;     // per-block partial rows + reduce_partials instead of atomics
     int chw;               // images, targets and grad_in are B x 3 x H x W (else B x H x W x 3)
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
@@ -245,7 +257,8 @@ hipError_t launch_fit_step(const float* partials, const double* partial_loss, in
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
                         float* rec, float* zero_grads, hipStream_t s, const float* bg_src = nullptr,
                         float* bg_dst = nullptr, const OrderArgs& o = OrderArgs{}, const int* halt = nullptr,
-                        RecordHead* head = nullptr, const RecordHead& head_val = RecordHead{});
+                        RecordHead* head = nullptr, const RecordHead& head_val = RecordHead{},
+                        double* pending = nullptr, int npending = 0);
 // n floats set to zero by a kernel (no memset node, so callers may capture it).
 hipError_t launch_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_forward(int mode, bool fast, const RasterArgs& a, hipStream_t s);

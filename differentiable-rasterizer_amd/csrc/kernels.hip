@@ -424,7 +424,8 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
                                                                const float* __restrict__ bg_src,
                                                                float* __restrict__ bg_dst, OrderArgs o,
                                                                const int* __restrict__ halt,
-                                                               RecordHead* __restrict__ head, RecordHead head_val) {
+                                                               RecordHead* __restrict__ head, RecordHead head_val,
+                                                               double* __restrict__ pending, int npending) {
     __shared__ int cells[ORD_MAX_CELLS];
     __shared__ __attribute__((aligned(16))) int hist[ORD_BUCKETS];
     if (halt && *halt >= 0) return;
@@ -433,6 +434,13 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
     if (head && b == 0 && part == 0 && threadIdx.x == 0) *head = head_val;
     // A record kept for a later backward holds its own copy of the backgrounds.
     if (bg_dst && part == 0 && threadIdx.x < 3) bg_dst[b * 3 + threadIdx.x] = bg_src[b * 3 + threadIdx.x];
+    // the scene's loss slots, pending until the fused kernel's tiles store
+    // theirs: from the last workgroup of the scene down, so that the records
+    // workgroups' idle threads take them before the order workgroup does
+    if (pending)
+        for (int i = ((int)gridDim.y - 1 - part) * (int)blockDim.x + (int)threadIdx.x; i < npending;
+             i += (int)(gridDim.y * blockDim.x))
+            pending[(size_t)b * npending + i] = __longlong_as_double((long long)LOSS_PENDING);
     if (!o.perm || part > 0) {
         // grid rows are capped at 65535: a records workgroup strides over the rest
         const int nparts = (int)gridDim.y - (o.perm ? 1 : 0);
@@ -1799,6 +1807,65 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(DET 
 // per block in wave order by sum_losses, as the four-wave blocks sum them.
 // Used where fused_kernel would be, outside the deterministic mode. ROWS: its
 // lists scan the tile row's triangles (RasterArgs::rows), else all of them.
+// The fused kernels' last B workgroups (RasterArgs::loss_tail): scene
+// b's loss from its tiles' partials once every slot holds one, in sum_losses'
+// order (per lane, blocks lane, lane + 64, ... each as its four tiles in wave
+// order; then the lanes summed), so the same bits as sum_losses. Every poll
+// loads the slots with device-scope atomic loads, which see the tiles'
+// device-scope atomic stores from any XCD. The wait is bounded: a scene whose
+// slots are still pending after TAIL_SPIN polls gets a NaN loss.
+constexpr int TAIL_U = 4;           // blocks per lane held in registers (scenes of up to 256 blocks)
+constexpr int TAIL_SPIN = 1 << 22;  // polls, each at least one round trip to memory
+__device__ inline double tail_load(const double* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool tail_pending(double v) { return (uint64_t)__double_as_longlong(v) == LOSS_PENDING; }
+
+__device__ inline void loss_tail(const RasterArgs& a, int b) {
+    const int lane = threadIdx.x & 63, nblk = a.gx * a.gy;
+    const double* pl = a.partial_loss + (size_t)b * nblk * WAVES;
+    const bool held = nblk <= 64 * TAIL_U;
+    double v[TAIL_U][WAVES];
+    bool ok = false;
+    for (int spin = 0; spin < TAIL_SPIN; spin++) {
+        bool pending = false;
+        if (held) {
+            for (int u = 0; u < TAIL_U; u++) {
+                const int r = lane + 64 * u;
+                for (int q = 0; q < WAVES; q++) {
+                    v[u][q] = r < nblk ? tail_load(pl + (size_t)r * WAVES + q) : 0.0;
+                    pending = pending || (r < nblk && tail_pending(v[u][q]));
+                }
+            }
+        } else {
+            for (int r = lane; r < nblk; r += 64)
+                for (int q = 0; q < WAVES; q++)
+                    pending = pending || tail_pending(tail_load(pl + (size_t)r * WAVES + q));
+        }
+        if (lane_mask(pending) == 0) {
+            ok = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    double l = 0.0;
+    if (held) {
+        for (int u = 0; u < TAIL_U; u++) {
+            double lb = v[u][0];
+            for (int q = 1; q < WAVES; q++) lb += v[u][q];
+            l = lane + 64 * u < nblk ? l + lb : l;
+        }
+    } else {
+        for (int r = lane; r < nblk; r += 64) {
+            double lb = tail_load(pl + (size_t)r * WAVES);
+            for (int q = 1; q < WAVES; q++) lb += tail_load(pl + (size_t)r * WAVES + q);
+            l += lb;
+        }
+    }
+    l = wave_sum_f64(l);
+    if (lane == 0) a.losses[b] = ok ? (float)(l / (3.0 * (double)a.H * (double)a.W)) : __builtin_nanf("");
+}
+
 template <int MODE, bool FAST, bool ROWS>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fused_tile_kernel(RasterArgs a, const float* __restrict__ records,
                                                                                 const TileEnt* __restrict__ ents) {
@@ -1806,6 +1873,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     __shared__ uint32_t list[CH];
     __shared__ __attribute__((aligned(16))) float trans[NP * TP];
     if (a.halt && *a.halt >= 0) return;
+    if (MODE == MODE_LOSS && a.loss_tail && (int)blockIdx.x >= (int)gridDim.x - a.B) {
+        loss_tail(a, (int)blockIdx.x - ((int)gridDim.x - a.B));
+        return;
+    }
     const int W = a.W, H = a.H, T = a.T;
     const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
@@ -1841,7 +1912,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     }
     if (MODE == MODE_LOSS) {
         l = wave_sum_f64(l);
-        if (lane == 0) a.partial_loss[tg.tile] = l;
+        if (lane == 0) {
+            if (a.loss_tail)
+                __hip_atomic_store(&a.partial_loss[tg.tile], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                a.partial_loss[tg.tile] = l;
+        }
     }
     // The entries this wave recorded with vector stores are read back below with
     // scalar loads: the stores are complete (in L2, which the scalar cache reads
@@ -1942,6 +2018,10 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
     extern __shared__ __attribute__((aligned(16))) float seg_lds[];
     SegEnt* const sent = reinterpret_cast<SegEnt*>(seg_lds);
     if (a.halt && *a.halt >= 0) return;
+    if (MODE == MODE_LOSS && !DET && a.loss_tail && (int)blockIdx.x >= (int)gridDim.x - a.B) {
+        if (threadIdx.x < 64) loss_tail(a, (int)blockIdx.x - ((int)gridDim.x - a.B));
+        return;
+    }
     const int W = a.W, H = a.H, T = a.T;
     const int s = (int)uniform_u32(threadIdx.x >> 6);  // this wave's segment
     const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0);
@@ -2052,7 +2132,12 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
     }
     if (MODE == MODE_LOSS && s == 0) {
         l = wave_sum_f64(l);
-        if (lane == 0) a.partial_loss[tg.tile] = l;
+        if (lane == 0) {
+            if (!DET && a.loss_tail)
+                __hip_atomic_store(&a.partial_loss[tg.tile], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                a.partial_loss[tg.tile] = l;
+        }
     }
     const bool plain = lane_mask(tot.z != 0 || tot.e != 0) == 0;  // the same in every wave
     __syncthreads();  // phase C reuses the SegEnt area
@@ -2402,8 +2487,9 @@ hipError_t launch_fit_step(const float* partials, const double* partial_loss, in
 
 hipError_t launch_setup(const float* params, int B, int T, int W, int H, float sigma, int setup_mode,
                         float* rec, float* zero_grads, hipStream_t s, const float* bg_src, float* bg_dst,
-                        const OrderArgs& o, const int* halt, RecordHead* head, const RecordHead& head_val) {
-    if (B == 0 || (T == 0 && !bg_dst && !o.perm && !head)) return hipSuccess;
+                        const OrderArgs& o, const int* halt, RecordHead* head, const RecordHead& head_val,
+                        double* pending, int npending) {
+    if (B == 0 || (T == 0 && !bg_dst && !o.perm && !head && !pending)) return hipSuccess;
     if (o.perm && (o.gy + 1) * (o.gx + 1) > ORD_MAX_CELLS) return hipErrorInvalidValue;
     // without an order, small workgroups spread the triangles over more CUs;
     // with one, a last workgroup per scene makes it
@@ -2418,7 +2504,7 @@ hipError_t launch_setup(const float* params, int B, int T, int W, int H, float s
     oa.c0_off = (0.5f - cs) / cs;
     oa.c1_off = -0.5f / cs;
     launch_k(setup_records, dim3(B, gx), dim3(n), 0, s, params, T, W, H, sigma, setup_mode, rec,
-                       zero_grads, bg_src, bg_dst, oa, halt, head, head_val);
+                       zero_grads, bg_src, bg_dst, oa, halt, head, head_val, pending, npending);
     return hipGetLastError();
 }
 
@@ -2493,7 +2579,10 @@ static void launch_fused_d(bool fast, const RasterArgs& a, dim3 grid, hipStream_
 template <int MODE>
 static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_t s) {
     if (a.segw) {
-        const dim3 tiles(grid.x * grid.y * grid.z * WAVES), threads(SEG_WAVES * 64);
+        // with the loss tail (not in the fixed-order mode), B more workgroups after the tiles
+        const dim3 tiles(grid.x * grid.y * grid.z * WAVES +
+                         (MODE == MODE_LOSS && !a.deterministic && a.loss_tail ? a.B : 0)),
+            threads(SEG_WAVES * 64);
         const size_t lds = seg_lds_bytes(a.deterministic != 0, a.T);
         if (a.deterministic && fast)
             launch_k((fused_seg_kernel<MODE, true, true, SEG_WAVES>), tiles, threads, lds, s, a, a.rec, a.tl_ent);
@@ -2509,7 +2598,8 @@ static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_
         launch_fused_d<MODE, true>(fast, a, grid, s);
         return;
     }
-    const dim3 tiles(grid.x * grid.y * grid.z * WAVES);
+    // with the loss tail, B more workgroups after the tiles
+    const dim3 tiles(grid.x * grid.y * grid.z * WAVES + (MODE == MODE_LOSS && a.loss_tail ? a.B : 0));
     const bool rows = a.rows && a.row_n;
     if (fast && rows)
         launch_k((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);

@@ -331,12 +331,16 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     if (bufs.order)
         ord = bufs.order_tiles ? drh::OrderArgs{bufs.order, 2 * (int)grid.x, 2 * (int)grid.y, 3, bufs.rows, bufs.row_n}
                                : drh::OrderArgs{bufs.order, (int)grid.x, (int)grid.y, 4};
+    // the fused kernels sum the losses themselves outside the fixed-order mode
+    // (RasterArgs::loss_tail): setup_records marks the loss slots pending
+    const bool loss_tail = bufs.fused && !det && mode == drh::MODE_LOSS && !(tail && tail->rec_ready);
     if (!(tail && tail->rec_ready)) {  // else the previous fit_step made this iteration's records
         KernelTimer kt(ctx, TK_SETUP, s, timed);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
                                   mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, bufs.rec,
                                   mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s, nullptr, nullptr,
-                                  ord, halt),
+                                  ord, halt, nullptr, drh::RecordHead{}, loss_tail ? bufs.ploss : nullptr,
+                                  nblk * drh::WAVES),
                 "setup_records launch");
     }
     drh::RasterArgs a{};
@@ -357,6 +361,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.tl_n = bufs.tn;
     a.grads = out_grads;
     a.losses = out_losses;
+    a.loss_tail = loss_tail ? 1 : 0;
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
     a.perm_fwd = T <= FWD_ORDER_MAX_T ? ord.perm : nullptr;
@@ -395,7 +400,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
                                    out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
                 "reduce_partials launch");
-    } else if (bufs.fused && mode == drh::MODE_LOSS) {
+    } else if (bufs.fused && mode == drh::MODE_LOSS && !loss_tail) {
         KernelTimer kt(ctx, TK_REDUCE, s, timed);
         HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, drh::loss_partials_per_block(true, false),
                                        3.0 * (double)H * (double)W, out_losses, s, halt),
