@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark: batched soft-raster forward + MSE + backward on one MI355X.
 
-One step = one drh_fused_loss_backward call (setup_records, fused_tile_kernel,
-sum_losses) over the headline workload: B=16 scenes at 256x256,
+One step = one drh_fused_loss_backward call (setup_records, then
+fused_tile_kernel, whose last workgroups also sum the scenes' losses) over the
+headline workload: B=16 scenes at 256x256,
 T=128 triangles each, sigma=0.0015, synthetic seeded scenes (diffrast.synth)
 and targets rendered from independently seeded scenes. Inputs and outputs
 stay in HBM; the timed region is K steps between two synchronizations.
@@ -126,8 +127,9 @@ def fused_kernel_name(B, H, W, T, deterministic=False):
 
 def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev, two_kernels=False):
     """Event-timed average duration of each kernel of the step: setup_records, then
-    either fused_kernel and sum_losses, or (two_kernels: DRH_UNFUSED=1, and the
-    paths that always take them) forward_kernel and backward_kernel."""
+    either the fused kernel (and sum_losses where it runs: fused kernels that
+    sum the losses themselves launch none), or (two_kernels: DRH_UNFUSED=1, and
+    the paths that always take them) forward_kernel and backward_kernel."""
     if two_kernels:
         os.environ["DRH_UNFUSED"] = "1"
     ctx.timing(True)
@@ -139,7 +141,10 @@ def kernel_times(torch, ctx, cfg, p, bg, targets, steps, dev, two_kernels=False)
         os.environ.pop("DRH_UNFUSED", None)
     ms = {f: t[f"{f}_ms"] / max(t[f"{f}_n"], 1) for f in ("setup", "raster", "backward", "reduce")}
     if t["backward_n"] == 0 and t["raster_n"] > 0:
-        return {"setup": ms["setup"], "fused": ms["raster"], "sum_losses": ms["reduce"]}
+        out = {"setup": ms["setup"], "fused": ms["raster"]}
+        if t["reduce_n"] > 0:
+            out["sum_losses"] = ms["reduce"]
+        return out
     return {"setup": ms["setup"], "forward": ms["raster"], "backward": ms["backward"], "reduce": ms["reduce"]}
 
 
