@@ -199,13 +199,9 @@ __device__ inline void reach_rows(const Reach r, const OrderArgs& o, int j, int 
     }
 }
 
-// Setup of triangle i (scene-major index): its record.
-__device__ inline void setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
-                                 int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
-    // The backward kernel adds into the gradients: they start at zero.
-    if (zero_grads)
-        for (int j = 0; j < NP; j++) zero_grads[i * NP + j] = 0.0f;
-    const float* p = params + i * NP;
+// The record of triangle i (scene-major index) from its parameters p.
+__device__ inline void setup_from(const float* __restrict__ p, size_t i, int W, int H, float sigma, int setup_mode,
+                                  float* __restrict__ rec) {
     float* r = rec + i * REC;
 
     float v[6];
@@ -316,6 +312,15 @@ __device__ inline void setup_one(const float* __restrict__ params, size_t i, int
         eb[6] = 0.0f;
         eb[7] = 0.0f;
     }
+}
+
+// Setup of triangle i: its record from params[i * NP ...].
+__device__ inline void setup_one(const float* __restrict__ params, size_t i, int W, int H, float sigma,
+                                 int setup_mode, float* __restrict__ rec, float* __restrict__ zero_grads) {
+    // The backward kernel adds into the gradients: they start at zero.
+    if (zero_grads)
+        for (int j = 0; j < NP; j++) zero_grads[i * NP + j] = 0.0f;
+    setup_from(params + i * NP, i, W, H, sigma, setup_mode, rec);
 }
 
 // The raster kernels' block order, heaviest first. A block's time follows its
@@ -2219,17 +2224,18 @@ __device__ inline double lane_block_losses(const double* __restrict__ pl, int nb
     return l;
 }
 
-// base[r * stride] for r in [r0, r1) added in order to 0, ROW_BATCH loads
+// base[r * stride] for r in [r0, r1) added in order to 0, BATCH loads (ROW_BATCH, or FIT_ROW_BATCH in fit_step)
 // issued before they are added.
-constexpr int ROW_BATCH = 8;
+constexpr int ROW_BATCH = 8, FIT_ROW_BATCH = 32;
+template <int BATCH = ROW_BATCH>
 __device__ inline float sum_rows_in_order(const float* __restrict__ base, size_t stride, int r0, int r1) {
     float acc = 0.0f;
-    for (int rr = r0; rr < r1; rr += ROW_BATCH) {
-        float v[ROW_BATCH];
+    for (int rr = r0; rr < r1; rr += BATCH) {
+        float v[BATCH];
 #pragma unroll
-        for (int u = 0; u < ROW_BATCH; u++) v[u] = base[(size_t)min(rr + u, r1 - 1) * stride];
+        for (int u = 0; u < BATCH; u++) v[u] = base[(size_t)min(rr + u, r1 - 1) * stride];
 #pragma unroll
-        for (int u = 0; u < ROW_BATCH; u++) acc = rr + u < r1 ? acc + v[u] : acc;
+        for (int u = 0; u < BATCH; u++) acc = rr + u < r1 ? acc + v[u] : acc;
     }
     return acc;
 }
@@ -2326,6 +2332,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
                                                            const double* __restrict__ partial_loss, int nblk,
                                                            int loss_per, int T, double npix3, FitTail ft) {
     __shared__ float part[RED_WAVES][64];
+    __shared__ float newp[FIT_TRIS * NP];  // the block's parameters after the update
     __shared__ int decision;
     const FitState cur = ft.st[ft.iter & 1];
     FitState* const nxt = ft.st + ((ft.iter + 1) & 1);
@@ -2351,7 +2358,9 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
     }
     float acc = 0.0f;
     if (mine)
-        acc = sum_rows_in_order(partials + col, cols, (nblk * wave) / RED_WAVES, (nblk * (wave + 1)) / RED_WAVES);
+        // the fit's rows (a few hundred tiles) in one round of loads per wave
+        acc = sum_rows_in_order<FIT_ROW_BATCH>(partials + col, cols, (nblk * wave) / RED_WAVES,
+                                               (nblk * (wave + 1)) / RED_WAVES);
     part[wave][lane] = acc;
     if (wave == 1) {
         const double s = wave_sum_f64(scene_loss(partial_loss, nblk, loss_per, lane));
@@ -2391,6 +2400,7 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
         float g = part[0][lane];
         for (int q = 1; q < RED_WAVES; q++) g += part[q][lane];
         ft.grads[col] = g;
+        float pn = p0;  // the parameter after this iteration
         if (d >= 0) {
             if (d & 1) ft.best[col] = p0;
             if (!(d & 2)) {
@@ -2405,16 +2415,19 @@ __global__ __launch_bounds__(RED_WAVES * 64) void fit_step(const float* __restri
                 else if (j < 9) pv = rust_clamp(pv, 0.0f, 1.0f);
                 else pv = rust_clamp(pv, 1e-3f, 0.999f);
                 ft.params[col] = pv;
+                pn = pv;
             }
         }
+        newp[lane] = pn;
     }
     if (ft.rec) {
         // the next iteration's records of the block's triangles, as
-        // setup_records would make them from the updated parameters
+        // setup_records would make them from the updated parameters (handed
+        // over in LDS instead of read back)
         __syncthreads();
         const int k = blockIdx.x * FIT_TRIS + (int)threadIdx.x;
         if ((int)threadIdx.x < FIT_TRIS && k < T)
-            setup_one(ft.params, (size_t)k, ft.W, ft.H, ft.sigma_next, SETUP_TAPE, ft.rec, nullptr);
+            setup_from(newp + threadIdx.x * NP, (size_t)k, ft.W, ft.H, ft.sigma_next, SETUP_TAPE, ft.rec);
     }
 }
 
