@@ -108,3 +108,37 @@ def test_record_keeps_a_bounded_number_of_entries(L, monkeypatch):
     assert n - (1 << 30) < B * T * 76 * 4 + B * H * W * 4 + tiles * 64 * 8 + tiles * 8 + tiles // 4 * 4 + 4096
     monkeypatch.setenv("DRH_MAX_TILE_ENTRIES", "7")
     assert L.record_bytes(2, 50, 16, 16) < L.record_bytes(2, 7, 16, 16) + 2 * 50 * 76 * 4
+
+
+def test_header_compiles_as_c_and_links_against_the_library(tmp_path):
+    # A C consumer's view of the boundary (what a cgo or other FFI binding
+    # sees): the header compiles as C99 without warnings, every declared
+    # entry point resolves when linked against the built library, and a
+    # host-only call answers.
+    import shutil
+    import subprocess
+
+    from diffrast import _lib
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    libdir = Path(_lib.LIB_PATH).parent
+    names = declared_symbols()
+    src = tmp_path / "consumer.c"
+    src.write_text(
+        '#include "diffrast_hip.h"\n#include <stdio.h>\n'
+        "typedef void (*fn)(void);\n"
+        "static const fn entry_points[] = {\n"
+        + "".join(f"    (fn){n},\n" for n in names)
+        + "};\n"
+        "int main(void) {\n"
+        '    printf("%d %d\\n", (int)(sizeof entry_points / sizeof entry_points[0]), drh_params_per_triangle());\n'
+        "    return 0;\n"
+        "}\n")
+    exe = tmp_path / "consumer"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", f"-I{ROOT / 'include'}", str(src),
+                    f"-L{libdir}", "-ldiffrast_hip", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True, timeout=120).stdout.split()
+    assert out == [str(len(names)), "10"]
