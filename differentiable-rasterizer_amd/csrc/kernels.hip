@@ -159,6 +159,8 @@ __device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sig
     return r;
 }
 
+constexpr int REACH_PAIR_ROWS = 8;  // cell rows of a box from which reach_rows walks pairs
+
 // Counts the cells the triangle can reach into the difference rows `cells`
 // (pitch ints per cell row), for cell rows j, j + m, ... of its cull box: in
 // each row, the run of cells whose pixel centres come within `far` of the
@@ -170,7 +172,12 @@ __device__ inline Reach make_reach(const float (&p)[NP], int W, int H, float sig
 // edges and its box, which are often most of them. r is taken by value: its
 // fields stay in registers over the rows.
 // With `rowmask` it also sets the triangle's bit k in the masks of every row of
-// its cull box (words 32-bit words per row).
+// its cull box (words 32-bit words per row). Without (no row lists: fewer than
+// 256 triangles, which are large), a triangle whose box spans REACH_PAIR_ROWS
+// or more cell rows takes them in pairs, each pair's run that of the two rows'
+// joint band, added to both: half the walk, which is the order workgroup's
+// longest phase for such triangles.
+template <bool MASKS>
 __device__ inline void reach_rows(const Reach r, const OrderArgs& o, int j, int m, int* cells, int pitch,
                                   uint32_t* rowmask, int words, int k) {
     const float cs = (float)(1 << o.shift), rH = o.r_h, cell_h = o.cell_h, wc = o.w_cells;
@@ -178,10 +185,12 @@ __device__ inline void reach_rows(const Reach r, const OrderArgs& o, int j, int 
     const float c0_off = o.c0_off, c1_off = o.c1_off;
     auto short_x = [&](float y) { return y <= r.ym ? fmaf(y - r.yt, r.s_tm, r.xt) : fmaf(y - r.ym, r.s_mb, r.xm); };
     const int x0 = r.x0(), x1 = r.x1(), y1 = r.y1();
-    for (int y = r.y0() + j; y <= y1; y += m) {
-        if (rowmask) atomicOr(&rowmask[y * words + (k >> 5)], 1u << (k & 31));
+    const int rows = !MASKS && y1 - r.y0() + 1 >= REACH_PAIR_ROWS ? 2 : 1;
+    const float bandr = band + (float)(rows - 1) * cell_h;
+    for (int y = r.y0() + rows * j; y <= y1; y += rows * m) {
+        if (MASKS) atomicOr(&rowmask[y * words + (k >> 5)], 1u << (k & 31));
         const float ya = fmaf((float)y, cell_h, y_first);
-        const float ca = fmaxf(ya, r.yt), cb = fminf(ya + band, r.yb);
+        const float ca = fmaxf(ya, r.yt), cb = fminf(ya + bandr, r.yb);
         if (!(ca <= cb)) continue;
         const float la = fmaf(ca - r.yt, r.s_tb, r.xt), lb = fmaf(cb - r.yt, r.s_tb, r.xt);
         const float sa = short_x(ca), sb = short_x(cb);
@@ -196,6 +205,10 @@ __device__ inline void reach_rows(const Reach r, const OrderArgs& o, int j, int 
         if (c0 > c1) continue;
         atomicAdd(&cells[y * pitch + c0], 1);
         atomicAdd(&cells[y * pitch + c1 + 1], -1);
+        if (!MASKS && rows == 2 && y + 1 <= y1) {
+            atomicAdd(&cells[(y + 1) * pitch + c0], 1);
+            atomicAdd(&cells[(y + 1) * pitch + c1 + 1], -1);
+        }
     }
 }
 
@@ -481,8 +494,12 @@ __global__ __launch_bounds__(SETUP_THREADS) void setup_records(const float* __re
         __syncthreads();
         // a power of two, so that the thread's triangle and row are a shift and a mask
         const int lg = 31 - __clz(min(SETUP_THREADS / nt, 16)), m = 1 << lg;
-        for (int w = threadIdx.x; w < nt * m; w += SETUP_THREADS)
-            reach_rows(reach[w >> lg], o, w & (m - 1), m, cells, pitch, rowmask, words, k0 + (w >> lg));
+        for (int w = threadIdx.x; w < nt * m; w += SETUP_THREADS) {
+            if (rowmask)
+                reach_rows<true>(reach[w >> lg], o, w & (m - 1), m, cells, pitch, rowmask, words, k0 + (w >> lg));
+            else
+                reach_rows<false>(reach[w >> lg], o, w & (m - 1), m, cells, pitch, nullptr, 0, 0);
+        }
         __syncthreads();
     }
     order_scene(o, cells, hist, b, T);
