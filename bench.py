@@ -33,6 +33,8 @@ that ramp; "sustained" reports the same step after 200 untimed steps beside it.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import re
@@ -69,6 +71,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+@contextlib.contextmanager
+def quiet_gc():
+    """A timed region without the cyclic garbage collector, as timeit runs its
+    loops: a full collection of this process (torch loaded) takes 30-45 ms and
+    would otherwise land inside whichever loop crosses its allocation count."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
 def box_cpu_share() -> int:
     try:
         return len(os.sched_getaffinity(0))
@@ -103,14 +120,15 @@ def time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev):
         ctx.fused_ptr(p.data_ptr(), bg.data_ptr(), targets.data_ptr(), B, T, H, W, SIGMA,
                       losses.data_ptr(), grads.data_ptr(), None, stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    with quiet_gc():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
     return ms, losses, grads
 
 
@@ -179,10 +197,11 @@ def timed_reps(fn, warmup=3, budget_s=0.4, min_reps=3, max_reps=50):
     for _ in range(warmup):
         fn()
     times = []
-    while (sum(times) < budget_s or len(times) < min_reps) and len(times) < max_reps:
-        t0 = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t0)
+    with quiet_gc():
+        while (sum(times) < budget_s or len(times) < min_reps) and len(times) < max_reps:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
     return times
 
 
@@ -218,10 +237,11 @@ def fit_gpu(ctx):
     init, bg = synth.seed_scene(target, T, 4)
     ctx.fit(target, init, bg, iters=20, patience=None)  # warm-up
     runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        r = ctx.fit(target, init, bg, iters=iters, patience=None)
-        runs.append(time.perf_counter() - t0)
+    with quiet_gc():
+        for _ in range(3):
+            t0 = time.perf_counter()
+            r = ctx.fit(target, init, bg, iters=iters, patience=None)
+            runs.append(time.perf_counter() - t0)
     dt = float(np.median(runs))
     ctx.timing(True)
     try:
@@ -290,12 +310,13 @@ def torch_op_ms(torch, cfg, p, targets, dev, steps=50):
     for _ in range(10):
         torch_layer.fused_mse(q, tgt, sigma=SIGMA).backward()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        q.grad = None
-        torch_layer.fused_mse(q, tgt, sigma=SIGMA).backward()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    with quiet_gc():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            q.grad = None
+            torch_layer.fused_mse(q, tgt, sigma=SIGMA).backward()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=50):
@@ -314,12 +335,13 @@ def torch_rasterize_ms(torch, cfg, p, targets, dev, keep_record=True, steps=50):
     for _ in range(10):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        q.grad = None
-        step()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    with quiet_gc():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            q.grad = None
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def forward_side(torch, ctx, dev, cpu=True):
@@ -357,17 +379,19 @@ def forward_side(torch, ctx, dev, cpu=True):
             run()
         torch.cuda.synchronize()
         n = 20
-        t0 = time.perf_counter()
-        for _ in range(n):
-            run()
-        torch.cuda.synchronize()
-        dev_ms = (time.perf_counter() - t0) * 1e3 / n
+        with quiet_gc():
+            t0 = time.perf_counter()
+            for _ in range(n):
+                run()
+            torch.cuda.synchronize()
+            dev_ms = (time.perf_counter() - t0) * 1e3 / n
         for _ in range(2):
             ctx.render(params, H, W, sig, bg)
-        t0 = time.perf_counter()
-        for _ in range(5):
-            ctx.render(params, H, W, sig, bg)
-        host_ms = (time.perf_counter() - t0) * 1e3 / 5
+        with quiet_gc():
+            t0 = time.perf_counter()
+            for _ in range(5):
+                ctx.render(params, H, W, sig, bg)
+            host_ms = (time.perf_counter() - t0) * 1e3 / 5
         res[name] = {"B": B, "H": H, "W": W, "T": T, "sigma": sig, "ms": round(dev_ms, 4),
                      "host_ms": round(host_ms, 4), "pixel_tri_per_s": B * H * W * T / (dev_ms / 1e3)}
         if name == "fwd_512_T1024":
