@@ -75,8 +75,9 @@ def log(*a):
 def quiet_gc():
     """A timed region without the cyclic garbage collector, as timeit runs its
     loops: a full collection of this process (torch loaded) takes 30-45 ms and
-    would otherwise land inside whichever loop crosses its allocation count."""
-    gc.collect()
+    would otherwise land inside whichever loop crosses its allocation count.
+    Nothing is collected on entry either: that would leave the GPU idle for as
+    long right before loops whose clocks have just ramped up."""
     was = gc.isenabled()
     gc.disable()
     try:
@@ -453,8 +454,9 @@ def gpu_leg(torch, ctx, name, dev, steps, warmup, two_kernels=True):
     cfg = synth.CONFIGS[name]
     B, H, W, T = cfg["B"], cfg["H"], cfg["W"], cfg["T"]
     params, p, bg, targets = make_inputs(torch, ctx, cfg, 1, dev)
-    ms, losses, grads = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)
-    kt = kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(steps, 50)), dev)
+    with quiet_gc():  # also between the timed steps and the event-timed ones
+        ms, losses, grads = time_fused(torch, ctx, cfg, p, bg, targets, steps, warmup, dev)
+        kt = kernel_times(torch, ctx, cfg, p, bg, targets, max(10, min(steps, 50)), dev)
     log(f"{name}: {ms:.4f} ms/batch over {steps} steps; kernel avg ms {kt}")
     # the same step on the two-kernel path, for its per-kernel figures
     two = None
