@@ -559,6 +559,19 @@ __device__ inline Rec load_rec(const float* __restrict__ r) {
     return Rec{v[0], v[1], *reinterpret_cast<const f8v*>(r + 32)};
 }
 
+// Triangle k's record by a 32-bit byte offset from its scene's records (a
+// scene holds at most 2^23 triangles, so T x REC x 4 bytes < 2^32): the scalar
+// loads take the offset as their SGPR offset, where a 64-bit index costs a
+// multiply-high and a carry add per entry. Entries of a tile's region likewise.
+__device__ inline uint32_t rec_off(uint32_t k) { return k * (uint32_t)(REC * sizeof(float)); }
+__device__ inline const float* rec_at(const float* __restrict__ rec, uint32_t off) {
+    return reinterpret_cast<const float*>(reinterpret_cast<const char*>(rec) + off);
+}
+__device__ inline TileEnt ent_at(const TileEnt* __restrict__ te, int i) {
+    return *reinterpret_cast<const TileEnt*>(reinterpret_cast<const char*>(te) +
+                                             (uint32_t)i * (uint32_t)sizeof(TileEnt));
+}
+
 // Field i0, i1 or i2 of the record for e = 0, 1, 2. The fields pass through an
 // empty asm that pins them to scalar registers: without it the compiler folds
 // the selects into one variable-index extract from the record vector, which it
@@ -697,21 +710,34 @@ enum : uint32_t { ENT_INBOX = 0x20 };
 // edges are strictly farther (by a margin well above rounding) at every pixel,
 // so the reference's first-minimum selection picks j with the same distance,
 // and the inside test reduces to the sign of c_j.
-// The record's block of the plan's edge (R_EB + 8 j, j = plan & 3; the
-// general plan's 3 reads edge 2's block, unused), loaded by the fast-path
-// sweeps together with the record: the asm keeps the load where it is, so its
-// scalar round trip is the record's instead of a second one inside the exact
-// path. In bounds for every record: R_EB + 24 == REC.
+// An entry's record (at byte offset `off`) and, for the fast-path sweeps, the
+// record's block of the plan's edge (R_EB + 8 j, j = plan & 3; the general
+// plan's 3 reads edge 2's block, unused), which the asm keeps where it is
+// issued: its scalar round trip is the record's instead of a second one inside
+// the exact path. WHOLE: the record's second half too, so that all of an
+// entry's loads issue together and it costs one scalar round trip; left to
+// itself the compiler sinks that load into the branch that first reads it, a
+// second round trip (and a 64-bit address add) for most entries. The sweeps
+// of the gradient kernels take WHOLE; forward_kernel's forward sweep does
+// not (its fast-path entries do not read the second half; +3.6 us at B=16
+// 128x128 T=128 with it). In bounds for every record: R_EB + 24 == REC.
 static_assert(R_EB + 24 == REC, "three 8-float edge blocks end the record");
-template <bool FAST>
-__device__ inline f8v edge_block(const float* __restrict__ rp, uint32_t plan) {
-    if (!FAST) return f8v{};
-    f8v eb = *reinterpret_cast<const f8v*>(rp + R_EB + 8 * min(plan & 3u, 2u));
-    asm volatile("" : "+s"(eb));
-    return eb;
+template <bool FAST, bool WHOLE>
+__device__ inline void load_entry(const float* __restrict__ rec, uint32_t off, uint32_t plan, Rec& r, f8v& eb) {
+    r = load_rec(rec_at(rec, off));
+    eb = f8v{};
+    if (FAST)
+        eb = *reinterpret_cast<const f8v*>(rec_at(rec, off + (uint32_t)(8 * sizeof(float)) * min(plan & 3u, 2u)) +
+                                           R_EB);
+    if (FAST && WHOLE)
+        asm volatile("" : "+s"(r.b), "+s"(eb));
+    else if (FAST)
+        asm volatile("" : "+s"(eb));
+    else if (WHOLE)
+        asm volatile("" : "+s"(r.b));
 }
 
-// The edge's fields come from its block of the record (edge_block).
+// The edge's fields come from its block of the record (load_entry).
 __device__ inline Geo geometry1(const Rec& r, const f8v& eb, Pix p, uint32_t plan) {
     const int j = (int)(plan & 3u);
     const float ax = eb[0], ay = eb[1], ex = eb[2], ey = eb[3], len2 = eb[4], rl = eb[5];
@@ -906,7 +932,7 @@ classify:
         if (c0 + lane < nc) {
             const uint32_t cd = list[c0 + lane];
             kl = cd >> 1;
-            const float* r = rec + (size_t)(kbase + (int)kl) * REC;
+            const float* r = rec_at(rec, rec_off((uint32_t)kbase + kl));
             const int flags = reinterpret_cast<const int*>(r)[R_FLAGS];
             // With MERGE the classification's fields, [R_N, R_EB), are loaded
             // together: the empty asm uses them all here, so that the compiler
@@ -1282,9 +1308,9 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
             const uint32_t ent = uniform_u32(nxt);
             nxt = lw[min(i + 1, CH - 1)];
             const int k = kbase + (int)(ent >> 8);
-            const float* rp = rec + (size_t)k * REC;
-            const Rec r = load_rec(rp);
-            const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
+            Rec r;
+            f8v eb;
+            load_entry<FAST, MERGE>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
             float w = 0.0f, cov;
             uint64_t bandm;
             Geo g;
@@ -1538,17 +1564,17 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
     // next entry is read one iteration ahead.
     auto recorded = [&](auto plain_c, int k0, int k1) {
         constexpr bool PLAIN = decltype(plain_c)::value;
-        TileEnt nx = te[min(i2, cap2 - 1)];
+        TileEnt nx = ent_at(te, min(i2, cap2 - 1));
         for (; i2 < i_end; i2++) {
             const TileEnt cur = nx;
             const int k = (int)(cur.k >> 8);
             if (k >= k1) break;
-            nx = te[min(i2 + 1, cap2 - 1)];
+            nx = ent_at(te, min(i2 + 1, cap2 - 1));
             const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
-            const float* rp = rec + (size_t)k * REC;
-            const Rec r = load_rec(rp);
-            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
+            Rec r;
+            f8v eb;
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
@@ -1593,9 +1619,9 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
             for (int i = 0; i < count; i++) {
                 const uint32_t ent = uniform_u32(lw[i]);
                 const int kl = (int)(ent >> 8);
-                const float* rp = rec + (size_t)(k0 + kl) * REC;
-                const Rec r = load_rec(rp);
-                const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
+                Rec r;
+                f8v eb;
+                load_entry<FAST, true>(rec, rec_off((uint32_t)(k0 + kl)), (ent >> 2) & 7u, r, eb);
                 float w = 0.0f, cov = 0.0f;
                 uint64_t bandm;
                 Geo g;
@@ -1961,12 +1987,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
         for (int i2 = 0; i2 < n2; i2++) {
             const TileEnt cur = nx;
             const int k = (int)(cur.k >> 8);
-            nx = te[min(i2 + 1, cap2 - 1)];
+            nx = ent_at(te, min(i2 + 1, cap2 - 1));
             const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
-            const float* rp = rec + (size_t)k * REC;
-            const Rec r = load_rec(rp);
-            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
+            Rec r;
+            f8v eb;
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
@@ -2072,9 +2098,9 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             const uint32_t ent = uniform_u32(nxt);
             nxt = list[s][min(i + 1, CH - 1)];
             const int k = kbase + (int)(ent >> 8);
-            const float* rp = rec + (size_t)k * REC;
-            const Rec r = load_rec(rp);
-            const f8v eb = edge_block<FAST>(rp, (ent >> 2) & 7u);
+            Rec r;
+            f8v eb;
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
             float w = 0.0f, cov;
             uint64_t bandm;
             Geo g;
@@ -2181,12 +2207,12 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
         for (int i2 = 0; i2 < n2; i2++) {
             const TileEnt cur = nx;
             const int k = (int)(cur.k >> 8);
-            nx = tr[min(i2 + 1, capS - 1)];
+            nx = ent_at(tr, min(i2 + 1, capS - 1));
             const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
-            const float* rp = rec + (size_t)k * REC;
-            const Rec r = load_rec(rp);
-            const f8v eb = edge_block<FAST>(rp, (cur.k >> 2) & 7u);
+            Rec r;
+            f8v eb;
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);

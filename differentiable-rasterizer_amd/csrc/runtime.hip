@@ -148,7 +148,7 @@ int check_sizes(int64_t B, int64_t T, int64_t H, int64_t W) {
     if (H == 0 || W == 0) return fail(DRH_ERR_INVALID_ARG, "height and width must be non-zero");
     if (B > 65535) return fail(DRH_ERR_TOO_LARGE, "batch of " + std::to_string(B) + " exceeds 65535 scenes per call");
     if (H > (1 << 20) || W > (1 << 20)) return fail(DRH_ERR_TOO_LARGE, "height and width are limited to 2^20");
-    if (T > (1 << 24)) return fail(DRH_ERR_TOO_LARGE, "more than 2^24 triangles per scene");
+    if (T > (1 << 23)) return fail(DRH_ERR_TOO_LARGE, "more than 2^23 triangles per scene");
     if (B * T > (int64_t)INT32_MAX / 64) return fail(DRH_ERR_TOO_LARGE, "batch x triangles too large for one call");
     return DRH_OK;
 }

@@ -40,7 +40,9 @@ enum {
     DRH_ERR_TIMEOUT = 2,     /* GpuError::Timeout: a host wait exceeded DRH_WAIT_TIMEOUT_S */
     DRH_ERR_DEVICE = 3,      /* GpuError::DeviceRequest: a HIP runtime failure */
     DRH_ERR_READBACK = 4,    /* GpuError::Readback: copying results to the host failed */
-    DRH_ERR_TOO_LARGE = 5,   /* GpuError::TooLarge: sizes beyond what one call supports */
+    DRH_ERR_TOO_LARGE = 5,   /* GpuError::TooLarge: sizes beyond what one call supports (more
+                                than 65535 scenes, 2^23 triangles per scene, 2^20 pixels a side,
+                                or B x T of 2^25 or more) */
     DRH_ERR_INVALID_ARG = 6  /* bad sigma, zero height/width, NULL pointer, bad config */
 };
 

@@ -98,6 +98,16 @@ def test_record_bytes_cover_every_part(L):
     assert e.value.code == 6
 
 
+def test_size_limits(L):
+    # the kernels address a scene's triangle records by 32-bit byte offsets
+    # (76 floats each): at most 2^23 triangles per scene
+    assert L.record_bytes(1, 1 << 23, 8, 8) > (1 << 23) * 76 * 4
+    for sizes in ((1, (1 << 23) + 1, 8, 8), (65536, 1, 8, 8), (1, 1, 8, (1 << 20) + 1), (4, 1 << 23, 8, 8)):
+        with pytest.raises(L.DiffrastError) as e:
+            L.record_bytes(*sizes)
+        assert e.value.code == 5, sizes
+
+
 def test_record_keeps_a_bounded_number_of_entries(L, monkeypatch):
     # past 1 GiB of entries the record keeps as many per tile as fit (at least 128)
     B, T, H, W = 16, 4096, 512, 512
