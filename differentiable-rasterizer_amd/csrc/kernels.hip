@@ -1303,68 +1303,74 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                                                 tg.cx1, tg.cy1, lw, lane, F_LIVE, &k1, ilist)
                             : 0;
         const int kbase = ilist ? 0 : k0;
-        uint32_t nxt = lw[0];  // the next entry is read one iteration ahead
-        for (int i = 0; i < count; i++) {
-            const uint32_t ent = uniform_u32(nxt);
-            nxt = lw[min(i + 1, CH - 1)];
-            const int k = kbase + (int)(ent >> 8);
-            Rec r;
-            f8v eb;
-            load_entry<FAST, MERGE>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
-            float w = 0.0f, cov;
-            uint64_t bandm;
-            Geo g;
-            const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
-            const bool on = __builtin_amdgcn_inverse_ballot_w64(onm);
-            // MODE_RECORD draws what a render draws but hands over what the
-            // taped forward keeps (F_TAPE); in the other modes the two agree.
-            const uint64_t tapedm = (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE)) ? onm : 0;
-            const bool taped = __builtin_amdgcn_inverse_ballot_w64(tapedm);
-            if (CKPT && tapedm != 0 && n2 == ck_at) {
-                // the colour and transmittance with which the backward sweep reaches this entry
-                float* c = ckw + (size_t)ck * (CKPT_WORDS * 64) + lane;
-                c[0] = col[0];
-                c[64] = col[1];
-                c[128] = col[2];
-                c[192] = tot.q;
-                c[256] = __int_as_float(tot.z);
-                c[320] = __int_as_float(tot.e);
-                ck++;
-                ck_at = ck < nck ? ck_at + a.seg_m : INT_MAX;
-            }
-            {
-                // raster.rs:60-66, kept only where the pair contributes, as
-                // col + w (c - col): one rounding fewer than c w + col (1 - w),
-                // and the form the backward kernel rebuilds the colour with
-                const float omw = 1.0f - w;
-                for (int ch = 0; ch < 3; ch++) {
-                    const float o = fmaf(w, r.f(R_C + ch) - col[ch], col[ch]);
-                    col[ch] = on ? o : col[ch];
+        // the list one half (64 entries) at a time, one entry per lane: each
+        // iteration takes its entry from its lane (v_readlane) instead of an LDS
+        // read, its address arithmetic and its wait
+        for (int h = 0; h < count; h += 64) {
+            const uint32_t held = lw[min(h + lane, CH - 1)];
+            const int nh = (int)uniform_u32((uint32_t)min(count - h, 64));
+            for (int i = 0; i < nh; i++) {
+                const uint32_t ent = (uint32_t)__builtin_amdgcn_readlane((int)held, i);
+                const int k = kbase + (int)(ent >> 8);
+                Rec r;
+                f8v eb;
+                load_entry<FAST, MERGE>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
+                float w = 0.0f, cov;
+                uint64_t bandm;
+                Geo g;
+                const uint64_t onm =
+                    pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+                const bool on = __builtin_amdgcn_inverse_ballot_w64(onm);
+                // MODE_RECORD draws what a render draws but hands over what the
+                // taped forward keeps (F_TAPE); in the other modes the two agree.
+                const uint64_t tapedm = (MODE != MODE_RECORD || (r.i(R_FLAGS) & F_TAPE)) ? onm : 0;
+                const bool taped = __builtin_amdgcn_inverse_ballot_w64(tapedm);
+                if (CKPT && tapedm != 0 && n2 == ck_at) {
+                    // the colour and transmittance with which the backward sweep reaches this entry
+                    float* c = ckw + (size_t)ck * (CKPT_WORDS * 64) + lane;
+                    c[0] = col[0];
+                    c[64] = col[1];
+                    c[128] = col[2];
+                    c[192] = tot.q;
+                    c[256] = __int_as_float(tot.z);
+                    c[320] = __int_as_float(tot.e);
+                    ck++;
+                    ck_at = ck < nck ? ck_at + a.seg_m : INT_MAX;
+                }
+                {
+                    // raster.rs:60-66, kept only where the pair contributes, as
+                    // col + w (c - col): one rounding fewer than c w + col (1 - w),
+                    // and the form the backward kernel rebuilds the colour with
+                    const float omw = 1.0f - w;
+                    for (int ch = 0; ch < 3; ch++) {
+                        const float o = fmaf(w, r.f(R_C + ch) - col[ch], col[ch]);
+                        col[ch] = on ? o : col[ch];
+                    }
+                    if (MODE != MODE_RENDER) {
+                        // trans_mul, by a plain product while it needs neither a zero
+                        // count nor a rescaling: a factor (in [0, 1], raster.rs:48)
+                        // that is zero, or a product below 2^-64 (or NaN), fails the
+                        // test, and only then does the wave take the counting step.
+                        const float f = taped ? omw : 1.0f;
+                        const float qn = tot.q * f;
+                        if (lane_mask(!(qn >= 5.421010862427522e-20f)) == 0)
+                            tot.q = qn;
+                        else
+                            trans_mul(tot, f);
+                    }
                 }
                 if (MODE != MODE_RENDER) {
-                    // trans_mul, by a plain product while it needs neither a zero
-                    // count nor a rescaling: a factor (in [0, 1], raster.rs:48)
-                    // that is zero, or a product below 2^-64 (or NaN), fails the
-                    // test, and only then does the wave take the counting step.
-                    const float f = taped ? omw : 1.0f;
-                    const float qn = tot.q * f;
-                    if (lane_mask(!(qn >= 5.421010862427522e-20f)) == 0)
-                        tot.q = qn;
-                    else
-                        trans_mul(tot, f);
-                }
-            }
-            if (MODE != MODE_RENDER) {
-                if (tapedm != 0) {
-                    if (n2 < cap2 && lane == 0) {
-                        TileEnt e;
-                        e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
-                        e.row = (ent >> 8) * (uint32_t)(NP * sizeof(float));
-                        e.on = tapedm;
-                        e.band = tapedm & bandm;
-                        te[n2] = e;
+                    if (tapedm != 0) {
+                        if (n2 < cap2 && lane == 0) {
+                            TileEnt e;
+                            e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
+                            e.row = (ent >> 8) * (uint32_t)(NP * sizeof(float));
+                            e.on = tapedm;
+                            e.band = tapedm & bandm;
+                            te[n2] = e;
+                        }
+                        n2++;
                     }
-                    n2++;
                 }
             }
         }
@@ -1625,7 +1631,8 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
                 float w = 0.0f, cov = 0.0f;
                 uint64_t bandm;
                 Geo g;
-                const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+                const uint64_t onm =
+                    pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
                 if (onm == 0) continue;
                 bandm &= onm;
                 const bool any_band = bandm != 0;
@@ -2093,35 +2100,39 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
                                   : 0;
         const int kbase = kb;
         kb = tg.live ? kend : k1;
-        uint32_t nxt = list[s][0];  // the next entry is read one iteration ahead
-        for (int i = 0; i < count; i++) {
-            const uint32_t ent = uniform_u32(nxt);
-            nxt = list[s][min(i + 1, CH - 1)];
-            const int k = kbase + (int)(ent >> 8);
-            Rec r;
-            f8v eb;
-            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
-            float w = 0.0f, cov;
-            uint64_t bandm;
-            Geo g;
-            const uint64_t onm = pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
-            if (onm == 0) continue;  // wave-uniform
-            SegEnt& e = sent[s * lcap + n2];
-            e.w[lane] = w;
-            if (lane == 0) {
-                e.c[0] = r.f(R_C);
-                e.c[1] = r.f(R_C + 1);
-                e.c[2] = r.f(R_C + 2);
-                e.on[0] = (uint32_t)onm;
-                e.on[1] = (uint32_t)(onm >> 32);
-                TileEnt t;
-                t.k = ((uint32_t)k << 8) | (ent & 0xFFu);
-                t.row = 0;
-                t.on = onm;
-                t.band = onm & bandm;
-                te[n2] = t;
+        // the list one half at a time, one entry per lane (as forward_sweep)
+        for (int h = 0; h < count; h += 64) {
+            const uint32_t held = list[s][min(h + lane, CH - 1)];
+            const int nh = (int)uniform_u32((uint32_t)min(count - h, 64));
+            for (int i = 0; i < nh; i++) {
+                const uint32_t ent = (uint32_t)__builtin_amdgcn_readlane((int)held, i);
+                const int k = kbase + (int)(ent >> 8);
+                Rec r;
+                f8v eb;
+                load_entry<FAST, true>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
+                float w = 0.0f, cov;
+                uint64_t bandm;
+                Geo g;
+                const uint64_t onm =
+                    pair_weight<FAST>(r, eb, ent, tg.x, tg.y, tg.p, validm, w, cov, bandm, g, rsig, sig);
+                if (onm == 0) continue;  // wave-uniform
+                SegEnt& e = sent[s * lcap + n2];
+                e.w[lane] = w;
+                if (lane == 0) {
+                    e.c[0] = r.f(R_C);
+                    e.c[1] = r.f(R_C + 1);
+                    e.c[2] = r.f(R_C + 2);
+                    e.on[0] = (uint32_t)onm;
+                    e.on[1] = (uint32_t)(onm >> 32);
+                    TileEnt t;
+                    t.k = ((uint32_t)k << 8) | (ent & 0xFFu);
+                    t.row = 0;
+                    t.on = onm;
+                    t.band = onm & bandm;
+                    te[n2] = t;
+                }
+                n2++;
             }
-            n2++;
         }
     }
     if (lane == 0) nent[s] = n2;
