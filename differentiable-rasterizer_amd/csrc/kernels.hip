@@ -572,16 +572,18 @@ __device__ inline TileEnt ent_at(const TileEnt* __restrict__ te, int i) {
                                              (uint32_t)i * (uint32_t)sizeof(TileEnt));
 }
 
-// Field i0, i1 or i2 of the record for e = 0, 1, 2. The fields pass through an
-// empty asm that pins them to scalar registers: without it the compiler folds
-// the selects into one variable-index extract from the record vector, which it
-// lowers to a copy of 16 fields into vector registers (uniform e) or a
-// 16-way compare chain (per-lane e). With it, a uniform e becomes s_cselect
-// and a per-lane e two v_cndmask.
-__device__ inline float pick3(const Rec& r, int e, int i0, int i1, int i2) {
-    float f0 = r.f(i0), f1 = r.f(i1), f2 = r.f(i2);
-    asm("" : "+s"(f0), "+s"(f1), "+s"(f2));
-    return e == 0 ? f0 : (e == 1 ? f1 : f2);
+// Field i0, i1 or i2 of the record for a per-lane e in {0, 1, 2}: the bits of
+// f_e as f0 ^ ((f0 ^ f1) & m1) ^ ((f0 ^ f2) & m2), m1 and m2 the lane masks of
+// e == 1 and e == 2 (its two bits, sign-extended). The two xors of scalar
+// fields are scalar; per lane it is two ands and a three-way xor, where a
+// select among scalar fields needs each field copied into a vector register
+// first (a vector instruction reads one scalar register at most): c2 -0.8 us
+// against the selects.
+__device__ inline float pick3_lane(const Rec& r, int e, int i0, int i1, int i2) {
+    const uint32_t b0 = __float_as_uint(r.f(i0));
+    const uint32_t x1 = b0 ^ __float_as_uint(r.f(i1)), x2 = b0 ^ __float_as_uint(r.f(i2));
+    const uint32_t m1 = (uint32_t)__builtin_amdgcn_sbfe(e, 0, 1), m2 = (uint32_t)__builtin_amdgcn_sbfe(e, 1, 1);
+    return __uint_as_float(b0 ^ (x1 & m1) ^ (x2 & m2));
 }
 
 struct Pix {
@@ -687,10 +689,10 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
         }
     }
     const int ed = g.edge;
-    g.ax = pick3(r, ed, R_V + 0, R_V + 2, R_V + 4);
-    g.ay = pick3(r, ed, R_V + 1, R_V + 3, R_V + 5);
-    g.ex = pick3(r, ed, R_E + 0, R_E + 2, R_E + 4);
-    g.ey = pick3(r, ed, R_E + 1, R_E + 3, R_E + 5);
+    g.ax = pick3_lane(r, ed, R_V + 0, R_V + 2, R_V + 4);
+    g.ay = pick3_lane(r, ed, R_V + 1, R_V + 3, R_V + 5);
+    g.ex = pick3_lane(r, ed, R_E + 0, R_E + 2, R_E + 4);
+    g.ey = pick3_lane(r, ed, R_E + 1, R_E + 3, R_E + 5);
     // sqrt is monotone, so sqrt(min d2) == min sqrt(d2) (raster.rs:97-99).
     g.dist = QUICK ? __builtin_amdgcn_sqrtf(best) : sqrtf(best);
     g.sd = inside ? g.dist : -g.dist;
