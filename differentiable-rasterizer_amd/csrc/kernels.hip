@@ -1690,6 +1690,33 @@ __device__ inline void reduce_entry_global(const float (&a)[NP], lds_float* tw, 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// reduce_entry_global for an entry with no band lane, whose vertex terms are
+// all zero (grad_pixel): only parameters 6-9 are summed. Lane 16p + g sums
+// pixels 4g..4g+3 of parameter 6 + p (one 16-byte read, three adds), the row
+// of sixteen partials is combined across its lanes (two quad steps, the
+// half-row and the row mirror) and lane 16p adds the total. About half of
+// c2's entries have no band lane: c2 -1.0 us.
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141;
+__device__ inline void reduce_entry_global_cw(const float (&a)[NP], lds_float* tw, float* grow, int lane) {
+    for (int q = 0; q < 4; q++) tw[q * TP + lane] = a[6 + q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int prm = lane >> 4, g = lane & 15;
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) f4v lds_f4v;
+    const f4v x = *reinterpret_cast<const lds_f4v*>(tw + prm * TP + 4 * g);
+    float sum = (x.x + x.y) + (x.z + x.w);
+    sum += dpp<DPP_XOR1>(sum);
+    sum += dpp<DPP_XOR2>(sum);
+    sum += dpp<DPP_ROW_HALF_MIRROR>(sum);
+    sum += dpp<DPP_ROW_MIRROR>(sum);
+    if (g == 0 && sum != 0.0f) unsafeAtomicAdd(grow + 6 + prm, sum);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Backward: the reverse-mode sweep (grad.rs:135-182) over the entries the
 // forward kernel recorded, again in scene order. The gradient reaching layer
 // k, d_canvas * prod_{j>k} (1 - w_j) (grad.rs:162-169), is formed as a ratio
@@ -2008,7 +2035,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
-            reduce_entry_global(part, tw, grads + (size_t)k * NP, lane);
+            if (cur.band != 0)
+                reduce_entry_global(part, tw, grads + (size_t)k * NP, lane);
+            else
+                reduce_entry_global_cw(part, tw, grads + (size_t)k * NP, lane);
         }
     };
     if (plain)
@@ -2234,8 +2264,10 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
             if (DET)
                 reduce_entry(part, tw, accs + (k - k0) * NP, lane);
-            else
+            else if (cur.band != 0)
                 reduce_entry_global(part, tw, grads + (size_t)k * NP, lane);
+            else
+                reduce_entry_global_cw(part, tw, grads + (size_t)k * NP, lane);
         }
     };
     if (plain)
