@@ -2080,7 +2080,6 @@ struct SegEnt {
     uint32_t pad[3];
 };
 static_assert(sizeof(SegEnt) == 288 && sizeof(SegEnt) % 16 == 0, "SegEnt keeps 16-byte alignment");
-constexpr int SEG_MAX = SEG_MAX_T / SEG_WAVES;  // triangles per segment
 
 // Triangles per segment (at most), the pitch of the segments' SegEnt records
 // in LDS; phase C's LDS bytes; and the workgroup's dynamic LDS.

@@ -204,12 +204,11 @@ float powi_f32(float a, int32_t b);
 // Brackets one kernel launch with events when the context is timing.
 class KernelTimer {
   public:
-    KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s, bool enabled = true);
+    KernelTimer(drh_ctx* ctx, int kernel, bool enabled = true);
     ~KernelTimer();
 
   private:
     drh_ctx* ctx_;
-    hipStream_t s_;
     TimedLaunch l_{};
     bool on_ = false;
 };

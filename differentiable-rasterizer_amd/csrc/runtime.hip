@@ -248,7 +248,7 @@ float powi_f32(float a, int32_t b) {
     return recip ? 1.0f / r : r;
 }
 
-KernelTimer::KernelTimer(drh_ctx* ctx, int kernel, hipStream_t s, bool enabled) : ctx_(ctx), s_(s) {
+KernelTimer::KernelTimer(drh_ctx* ctx, int kernel, bool enabled) : ctx_(ctx) {
     if (!enabled || !ctx->timing) return;
     l_.kernel = kernel;
     if (hipEventCreate(&l_.start) != hipSuccess) return;
@@ -335,7 +335,7 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     // (RasterArgs::loss_tail): setup_records marks the loss slots pending
     const bool loss_tail = bufs.fused && !det && mode == drh::MODE_LOSS && !(tail && tail->rec_ready);
     if (!(tail && tail->rec_ready)) {  // else the previous fit_step made this iteration's records
-        KernelTimer kt(ctx, TK_SETUP, s, timed);
+        KernelTimer kt(ctx, TK_SETUP, timed);
         HIP_TRY(drh::launch_setup(params, B, T, W, H, sigma,
                                   mode == drh::MODE_RENDER ? drh::SETUP_RENDER : drh::SETUP_TAPE, bufs.rec,
                                   mode != drh::MODE_RENDER && !det ? out_grads : nullptr, s, nullptr, nullptr,
@@ -378,30 +378,30 @@ int run_raster_bufs(drh_ctx* ctx, int mode, const float* params, const float* bg
     a.gy = (int)grid.y;
     a.ckpt = bufs.ckpt;
     if (bufs.fused) {
-        KernelTimer kt(ctx, TK_RASTER, s, timed);
+        KernelTimer kt(ctx, TK_RASTER, timed);
         HIP_TRY(drh::launch_fused(mode, fast, a, s), "fused_kernel launch");
     } else {
         {
-            KernelTimer kt(ctx, TK_RASTER, s, timed);
+            KernelTimer kt(ctx, TK_RASTER, timed);
             HIP_TRY(drh::launch_forward(mode, fast, a, s), "forward_kernel launch");
         }
         if (mode == drh::MODE_RENDER) return DRH_OK;
-        KernelTimer kt(ctx, TK_BACKWARD, s, timed);
+        KernelTimer kt(ctx, TK_BACKWARD, timed);
         HIP_TRY(drh::launch_backward(mode, fast, bufs.cap2 < T, a, s), "backward_kernel launch");
     }
     if (det && tail) {
-        KernelTimer kt(ctx, TK_ADAM, s, timed);
+        KernelTimer kt(ctx, TK_ADAM, timed);
         HIP_TRY(drh::launch_fit_step(a.partials, a.partial_loss, nrows, nrows / nblk, T, 3.0 * (double)H * (double)W,
                                      *tail, s),
                 "fit_step launch");
     } else if (det) {
-        KernelTimer kt(ctx, TK_REDUCE, s, timed);
+        KernelTimer kt(ctx, TK_REDUCE, timed);
         HIP_TRY(drh::launch_reduce(a.partials, a.partial_loss, B, nrows, nrows / nblk, T, 3.0 * (double)H * (double)W,
                                    out_grads,
                                    mode == drh::MODE_LOSS ? out_losses : nullptr, s, halt),
                 "reduce_partials launch");
     } else if (bufs.fused && mode == drh::MODE_LOSS && !loss_tail) {
-        KernelTimer kt(ctx, TK_REDUCE, s, timed);
+        KernelTimer kt(ctx, TK_REDUCE, timed);
         HIP_TRY(drh::launch_sum_losses(a.partial_loss, B, nblk, drh::loss_partials_per_block(true, false),
                                        3.0 * (double)H * (double)W, out_losses, s, halt),
                 "sum_losses launch");
@@ -909,7 +909,7 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
     a.gy = (int)grid.y;
     a.nseg = 1;
     {
-        KernelTimer kt(ctx, TK_SETUP, s);
+        KernelTimer kt(ctx, TK_SETUP);
         const drh::RecordHead head = make_head(B, T, H, W, sigma, flags);
         HIP_TRY(drh::launch_setup(p.dev, a.B, a.T, a.W, a.H, sigma, drh::SETUP_RECORD, const_cast<float*>(a.rec),
                                   nullptr, s, bg.dev, const_cast<float*>(a.bg), ord, nullptr,
@@ -918,7 +918,7 @@ int drh_render_record(drh_ctx* ctx, const float* params, const float* background
         remember_record(ctx, record, head);
     }
     {
-        KernelTimer kt(ctx, TK_RASTER, s);
+        KernelTimer kt(ctx, TK_RASTER);
         HIP_TRY(drh::launch_forward(drh::MODE_RECORD, !(flags & DRH_EXACT_MATH), a, s), "forward_kernel launch");
     }
     if ((rc = copy_back(img, s))) return rc;
@@ -969,16 +969,16 @@ int drh_backward_recorded(drh_ctx* ctx, const void* record, uint64_t record_byte
     a.deterministic = det ? 1 : 0;
     a.chw = (flags & DRH_CHANNELS_FIRST) ? 1 : 0;
     if (!det) {
-        KernelTimer kt(ctx, TK_SETUP, s);
+        KernelTimer kt(ctx, TK_SETUP);
         HIP_TRY(drh::launch_zero(grads.dev, (size_t)B * T * NP, s), "zero_floats launch");
     }
     {
-        KernelTimer kt(ctx, TK_BACKWARD, s);
+        KernelTimer kt(ctx, TK_BACKWARD);
         HIP_TRY(drh::launch_backward(drh::MODE_GRAD_IN, !(flags & DRH_EXACT_MATH), L.cap2 < T, a, s),
                 "backward_kernel launch");
     }
     if (det) {
-        KernelTimer kt(ctx, TK_REDUCE, s);
+        KernelTimer kt(ctx, TK_REDUCE);
         HIP_TRY(drh::launch_reduce(a.partials, nullptr, a.B, nblk, 1, a.T, 3.0 * a.H * (double)a.W, grads.dev, nullptr, s),
                 "reduce_partials launch");
     }
@@ -1012,7 +1012,7 @@ int drh_adam_project_step(drh_ctx* ctx, float* params, const float* grads, float
     float* dm = const_cast<float*>(min_.dev);
     float* dv = const_cast<float*>(vin.dev);
     {
-        KernelTimer kt(ctx, TK_ADAM, s);
+        KernelTimer kt(ctx, TK_ADAM);
         HIP_TRY(drh::launch_adam(dp, g.dev, dm, dv, l.dev, (int)n, beta1, beta2, eps, bc1, bc2, project, s),
                 "adam_project launch");
     }
