@@ -1366,11 +1366,16 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                         if (n2 < cap2 && lane == 0) {
                             TileEnt e;
                             e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
-                            e.row = (ent >> 8) * (uint32_t)(NP * sizeof(float));
+                            // the merged lists' consumer (fused_tile_kernel) reads no row
+                            e.row = MERGE ? 0u : (ent >> 8) * (uint32_t)(NP * sizeof(float));
                             e.on = tapedm;
                             e.band = tapedm & bandm;
-                            te[n2] = e;
+                            *te = e;
                         }
+                        // entry n2 + 1, stored only while n2 < cap2: a running pointer
+                        // instead of an index's 64-bit multiply-add (with the merged
+                        // lists' constant row: -1.4 us of ~88 at B=16 256x256 T=128)
+                        te++;
                         n2++;
                     }
                 }
