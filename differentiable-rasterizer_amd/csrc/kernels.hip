@@ -1363,18 +1363,21 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                 }
                 if (MODE != MODE_RENDER) {
                     if (tapedm != 0) {
-                        if (n2 < cap2 && lane == 0) {
+                        // With merged lists (fused_tile_kernel) the region holds every
+                        // entry (cap2 >= T: the fused path's condition), and every lane
+                        // stores the same (wave-uniform) entry: no lane mask to set up
+                        if (MERGE || (n2 < cap2 && lane == 0)) {
                             TileEnt e;
-                            e.k = ((uint32_t)k << 8) | (ent & 0xFFu);
-                            // the merged lists' consumer (fused_tile_kernel) reads no row
+                            e.k = ent + ((uint32_t)kbase << 8);  // (k << 8) | the entry's low byte
+                            // the merged lists' consumer reads no row
                             e.row = MERGE ? 0u : (ent >> 8) * (uint32_t)(NP * sizeof(float));
                             e.on = tapedm;
                             e.band = tapedm & bandm;
                             *te = e;
                         }
                         // entry n2 + 1, stored only while n2 < cap2: a running pointer
-                        // instead of an index's 64-bit multiply-add (with the merged
-                        // lists' constant row: -1.4 us of ~88 at B=16 256x256 T=128)
+                        // instead of an index's 64-bit multiply-add. With the constant row
+                        // -1.4 us of ~88 at B=16 256x256 T=128, with the rest -1.3 more
                         te++;
                         n2++;
                     }
