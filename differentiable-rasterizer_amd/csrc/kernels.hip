@@ -704,8 +704,11 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
 // tile and the other two edge lines stay clear of it, so the signs of their
 // cross products are the same at every pixel (inner side when PLAN_INNER).
 enum : uint32_t { PLAN_GENERAL = 3, PLAN_INNER = 4 };
-// Entry bit: the tile lies inside the triangle's box (no per-pixel box test).
-enum : uint32_t { ENT_INBOX = 0x20 };
+// Entry bits 5-6: the byte offset, within the record's edge blocks, of the
+// plan's block (32 min(plan & 3, 2)), so that a sweep addresses it with one
+// bitwise and. Entry bit 7: the tile lies inside the triangle's box (no
+// per-pixel box test).
+enum : uint32_t { ENT_EB = 0x60, ENT_INBOX = 0x80 };
 
 // geometry<true> for a single-edge plan: the reference's distance to edge j
 // and its cross product, with the other edges' results known. The excluded
@@ -714,7 +717,8 @@ enum : uint32_t { ENT_INBOX = 0x20 };
 // and the inside test reduces to the sign of c_j.
 // An entry's record (at byte offset `off`) and, for the fast-path sweeps, the
 // record's block of the plan's edge (R_EB + 8 j, j = plan & 3; the general
-// plan's 3 reads edge 2's block, unused), which the asm keeps where it is
+// plan's 3 reads edge 2's block, unused; `code` is the entry's low byte, whose
+// ENT_EB bits hold the block's byte offset), which the asm keeps where it is
 // issued: its scalar round trip is the record's instead of a second one inside
 // the exact path. WHOLE: the record's second half too, so that all of an
 // entry's loads issue together and it costs one scalar round trip; left to
@@ -725,12 +729,10 @@ enum : uint32_t { ENT_INBOX = 0x20 };
 // 128x128 T=128 with it). In bounds for every record: R_EB + 24 == REC.
 static_assert(R_EB + 24 == REC, "three 8-float edge blocks end the record");
 template <bool FAST, bool WHOLE>
-__device__ inline void load_entry(const float* __restrict__ rec, uint32_t off, uint32_t plan, Rec& r, f8v& eb) {
+__device__ inline void load_entry(const float* __restrict__ rec, uint32_t off, uint32_t code, Rec& r, f8v& eb) {
     r = load_rec(rec_at(rec, off));
     eb = f8v{};
-    if (FAST)
-        eb = *reinterpret_cast<const f8v*>(rec_at(rec, off + (uint32_t)(8 * sizeof(float)) * min(plan & 3u, 2u)) +
-                                           R_EB);
+    if (FAST) eb = *reinterpret_cast<const f8v*>(rec_at(rec, off + (code & ENT_EB)) + R_EB);
     if (FAST && WHOLE)
         asm volatile("" : "+s"(r.b), "+s"(eb));
     else if (FAST)
@@ -1028,7 +1030,7 @@ classify:
         if (cls != 0) {
             const int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = (kl << 8) | extra | (plan << 2) | cls;
+            list[pos] = (kl << 8) | extra | (min(plan & 3u, 2u) << 5) | (plan << 2) | cls;
         }
         count += (int)__popcll(mask);
     }
@@ -1316,7 +1318,7 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                 const int k = kbase + (int)(ent >> 8);
                 Rec r;
                 f8v eb;
-                load_entry<FAST, MERGE>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
+                load_entry<FAST, MERGE>(rec, rec_off((uint32_t)k), ent, r, eb);
                 float w = 0.0f, cov;
                 uint64_t bandm;
                 Geo g;
@@ -1590,7 +1592,7 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             Rec r;
             f8v eb;
-            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
@@ -1637,7 +1639,7 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
                 const int kl = (int)(ent >> 8);
                 Rec r;
                 f8v eb;
-                load_entry<FAST, true>(rec, rec_off((uint32_t)(k0 + kl)), (ent >> 2) & 7u, r, eb);
+                load_entry<FAST, true>(rec, rec_off((uint32_t)(k0 + kl)), ent, r, eb);
                 float w = 0.0f, cov = 0.0f;
                 uint64_t bandm;
                 Geo g;
@@ -2036,7 +2038,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             Rec r;
             f8v eb;
-            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
@@ -2148,7 +2150,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
                 const int k = kbase + (int)(ent >> 8);
                 Rec r;
                 f8v eb;
-                load_entry<FAST, true>(rec, rec_off((uint32_t)k), (ent >> 2) & 7u, r, eb);
+                load_entry<FAST, true>(rec, rec_off((uint32_t)k), ent, r, eb);
                 float w = 0.0f, cov;
                 uint64_t bandm;
                 Geo g;
@@ -2262,7 +2264,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             Rec r;
             f8v eb;
-            load_entry<FAST, true>(rec, rec_off((uint32_t)k), (cur.k >> 2) & 7u, r, eb);
+            load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
             float cov = 1.0f;
             Geo g;
             if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
