@@ -74,7 +74,7 @@ constexpr uint64_t LOSS_PENDING = 0xFFF4C0DE5EED0001ull;
 // One recorded entry of a tile's list, written by the forward kernel and read
 // (with scalar loads) by the backward kernel.
 struct TileEnt {
-    uint32_t k;     // (k << 8) | (plan << 2) | class, k the triangle index
+    uint32_t k;     // (k << 8) | the list entry's low byte (class, plan, edge-block offset, in-box bit)
     uint32_t row;   // byte offset of the triangle's row in a chunk's per-wave accumulator
     uint64_t on;    // lanes with w > MIN_WEIGHT
     uint64_t band;  // of those, lanes on the exact path
