@@ -37,7 +37,7 @@ enum RecField : int {
     R_D = 40,      // 6: unit edge directions (fast path only)
     R_SOFF = 46,   // 3: a . d per edge
     R_LEN = 49,    // 3: |e|
-    R_EB = 52,     // 3 x 8: per edge a.x a.y e.x e.y |e|^2 1/|e|^2 0 0 (scalar-loaded by edge index)
+    R_EB = 52,     // 3 x 8: per edge a.x a.y e.x e.y |e|^2 1/|e|^2 (+-1: F_CCW) 0 (scalar-loaded by edge index)
 };
 // F_CCW: the cross products of inside points are >= 0 (else <= 0).
 // F_LIVE: drawn by this call's forward pass. F_TAPE: live for the taped forward

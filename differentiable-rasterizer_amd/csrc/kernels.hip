@@ -322,7 +322,7 @@ __device__ inline void setup_from(const float* __restrict__ p, size_t i, int W, 
         eb[3] = e[2 * j + 1];
         eb[4] = len2[j];
         eb[5] = rlen2[j];
-        eb[6] = 0.0f;
+        eb[6] = area2 >= 0.0f ? 1.0f : -1.0f;  // F_CCW as a factor: c eb[6] >= 0 inside
         eb[7] = 0.0f;
     }
 }
@@ -756,7 +756,7 @@ __device__ inline Geo geometry1(const Rec& r, const f8v& eb, Pix p, uint32_t pla
     const float dy = apy - g.t * ey;
     g.dist = __builtin_amdgcn_sqrtf(dx * dx + dy * dy);
     // c <= 0 is -c >= 0, also for c = +-0
-    const float cs = (r.i(R_FLAGS) & F_CCW) ? c : -c;
+    const float cs = c * eb[6];  // the orientation flag as an exact factor of +-1
     const bool inside = (plan & PLAN_INNER) && cs >= 0.0f;
     g.sd = inside ? g.dist : -g.dist;
     g.edge = j;
