@@ -153,6 +153,9 @@ struct RasterArgs {
     const int* perm_fwd;   // block order of the forward kernel (OrderArgs::perm) or null
     const int* perm_bwd;   // block order of the backward kernel or null
     int perm_tiles;        // perm_bwd orders 8x8 tiles (one-wave fused kernel), not blocks
+    // ceil(2^32 / (2 gx)), set by the one-wave fused kernel's launch: an ordered
+    // tile's row in its scene's tile grid by one multiply-high instead of a division
+    uint32_t tdiv_m;
     // OrderArgs::rows / row_n of 8x8-tile rows (row_gy per scene), or null:
     // the one-wave fused kernel's lists then scan every triangle
     const int* rows;

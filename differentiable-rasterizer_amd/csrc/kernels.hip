@@ -1208,11 +1208,17 @@ __device__ inline TileGeo tile_geo(int W, int H, const int* perm = nullptr, int 
 // first) run in consecutive slots; without perm, block order.
 // With perm_tiles, perm orders the scene's 2gx x 2gy tiles: slot i is tile
 // rank i / B of scene i % B.
-__device__ inline TileGeo tile_geo_wave(int W, int H, int gx, int gy, const int* perm, int B, bool perm_tiles) {
+__device__ inline TileGeo tile_geo_wave(int W, int H, int gx, int gy, const int* perm, int B, bool perm_tiles,
+                                        uint32_t tdiv_m = 0) {
     const int nb = gx * gy, i = (int)blockIdx.x;
     if (perm && perm_tiles) {
-        const int nt = nb * WAVES, b = i % B, rank = i / B;
-        const int t = min(max(perm[(size_t)b * nt + rank], 0), nt - 1), tx = t % (2 * gx), ty = t / (2 * gx);
+        // A two-dimensional grid (the one-wave fused kernel) has the scene in x
+        // and the rank in y, the same dispatch order as slot i = rank B + b.
+        const bool xy = gridDim.y > 1;
+        const int nt = nb * WAVES, b = xy ? (int)blockIdx.x : i % B, rank = xy ? (int)blockIdx.y : i / B;
+        const int t = min(max(perm[(size_t)b * nt + rank], 0), nt - 1);
+        // t / (2 gx) by tdiv_m: exact while t 2 gx < 2^32 (the order's cells fit in LDS)
+        const int ty = tdiv_m ? (int)__umulhi((uint32_t)t, tdiv_m) : t / (2 * gx), tx = t - ty * (2 * gx);
         return tile_at(W, H, gx, gy, b, tx >> 1, ty >> 1, rank, 0, 1, (ty & 1) * 2 + (tx & 1));
     }
     const int wave = i % WAVES;
@@ -1967,12 +1973,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     __shared__ uint32_t list[CH];
     __shared__ __attribute__((aligned(16))) float trans[NP * TP];
     if (a.halt && *a.halt >= 0) return;
-    if (MODE == MODE_LOSS && a.loss_tail && (int)blockIdx.x >= (int)gridDim.x - a.B) {
-        loss_tail(a, (int)blockIdx.x - ((int)gridDim.x - a.B));
-        return;
+    if (MODE == MODE_LOSS && a.loss_tail) {
+        // the last B workgroups: the last row of a two-dimensional grid
+        if (gridDim.y > 1 ? blockIdx.y == gridDim.y - 1 : (int)blockIdx.x >= (int)gridDim.x - a.B) {
+            loss_tail(a, gridDim.y > 1 ? (int)blockIdx.x : (int)blockIdx.x - ((int)gridDim.x - a.B));
+            return;
+        }
     }
     const int W = a.W, H = a.H, T = a.T;
-    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0);
+    const TileGeo tg = tile_geo_wave(W, H, a.gx, a.gy, a.perm_bwd, a.B, a.perm_tiles != 0, a.tdiv_m);
     const uint64_t validm = lane_mask(tg.valid);  // lanes whose pixel is in the image
     const int lane = tg.lane, b = tg.b;
     const float sig = fmaxf(a.sigma, 1e-8f);
@@ -2708,17 +2717,24 @@ static void launch_fused_m(bool fast, const RasterArgs& a, dim3 grid, hipStream_
         launch_fused_d<MODE, true>(fast, a, grid, s);
         return;
     }
-    // with the loss tail, B more workgroups after the tiles
-    const dim3 tiles(grid.x * grid.y * grid.z * WAVES + (MODE == MODE_LOSS && a.loss_tail ? a.B : 0));
+    // with the loss tail, B more workgroups after the tiles. With an order of
+    // tiles: scenes in x and ranks in y (no division in the kernel), the loss
+    // tail the last row.
+    const bool tail = MODE == MODE_LOSS && a.loss_tail;
+    const unsigned nt = grid.x * grid.y * WAVES;  // tiles per scene
+    const bool xy = a.perm_bwd && a.perm_tiles && nt + 1 <= 65535u;
+    const dim3 tiles = xy ? dim3((unsigned)a.B, nt + (tail ? 1u : 0u)) : dim3(nt * grid.z + (tail ? a.B : 0));
+    RasterArgs b = a;
+    b.tdiv_m = xy ? (uint32_t)((0xFFFFFFFFull + 2ull * a.gx) / (2ull * a.gx)) : 0u;
     const bool rows = a.rows && a.row_n;
     if (fast && rows)
-        launch_k((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, true, true>), tiles, dim3(64), 0, s, b, b.rec, b.tl_ent);
     else if (fast)
-        launch_k((fused_tile_kernel<MODE, true, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, true, false>), tiles, dim3(64), 0, s, b, b.rec, b.tl_ent);
     else if (rows)
-        launch_k((fused_tile_kernel<MODE, false, true>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, false, true>), tiles, dim3(64), 0, s, b, b.rec, b.tl_ent);
     else
-        launch_k((fused_tile_kernel<MODE, false, false>), tiles, dim3(64), 0, s, a, a.rec, a.tl_ent);
+        launch_k((fused_tile_kernel<MODE, false, false>), tiles, dim3(64), 0, s, b, b.rec, b.tl_ent);
 }
 
 hipError_t launch_fused(int mode, bool fast, const RasterArgs& a, hipStream_t s) {
