@@ -24,6 +24,11 @@ HEADERS = [CSRC / "kernels.h", CSRC / "runtime.h", ROOT / "include" / "diffrast_
 # -ffp-contract=off: the kernels state every FMA explicitly; plain a*b+c must
 # round twice, as the reference's arithmetic does.
 # -packed-fp32-ops: no v_pk_*_f32 instructions in the generated code.
+# -structurizecfg-skip-uniform-regions: regions whose branches are all
+# wave-uniform (scalar-condition branches) keep their control flow as written;
+# the default structurizer rewrites them as it does divergent ones, carrying
+# path flags (scalar mask operations and extra branches) through the sweeps'
+# per-entry code. Regions with a divergent branch are structurized as before.
 FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -32,6 +37,7 @@ FLAGS = [
     "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-structurizecfg-skip-uniform-regions=true",
     "-Wall",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",

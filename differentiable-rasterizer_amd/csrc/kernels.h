@@ -65,6 +65,10 @@ constexpr int CAP2_MIN = 128;
 // 176x176 T=150 fit: 26.4 -> 23.4 us per iteration).
 constexpr int SEG_WAVES = 8;
 constexpr int SEG_MAX_T = 160;
+// Its entry region per tile: SEG_WAVES segments of whole 64-byte lines (8
+// entries) of more than T / SEG_WAVES entries each, so that cap2 > T, as the
+// fused paths require.
+__host__ __device__ constexpr int seg_cap2(int T) { return SEG_WAVES * (((T + SEG_WAVES - 1) / SEG_WAVES + 8) & ~7); }
 // A loss slot not yet written (RasterArgs::loss_tail): a signalling NaN with
 // the lowest mantissa bit set. Arithmetic only returns quiet NaNs, and NaNs
 // that reach the loss from float inputs have their low 29 mantissa bits clear,
@@ -74,7 +78,7 @@ constexpr uint64_t LOSS_PENDING = 0xFFF4C0DE5EED0001ull;
 // One recorded entry of a tile's list, written by the forward kernel and read
 // (with scalar loads) by the backward kernel.
 struct TileEnt {
-    uint32_t k;     // (k << 8) | the list entry's low byte (class, plan, edge-block offset, in-box bit)
+    uint32_t k;     // (k << 8) | the list entry's low byte (kind bits, plan, edge-block offset, in-box bit)
     uint32_t row;   // byte offset of the triangle's row in a chunk's per-wave accumulator
     uint64_t on;    // lanes with w > MIN_WEIGHT
     uint64_t band;  // of those, lanes on the exact path

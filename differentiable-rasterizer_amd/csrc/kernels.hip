@@ -678,15 +678,17 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
             g.t = t;
         }
     }
+    // Near ties are rare; the wave takes the square roots at every lane when
+    // any lane has one (a wave-uniform branch, so no divergent control flow
+    // for the compiler to thread path flags through), and the others keep
+    // their edge. Edge 0 wins over edge 1, as the first minimum.
     const float near = best * 1.0000005f;
-    if ((g.edge > 0 && d2v[0] <= near) || (g.edge > 1 && d2v[1] <= near)) {
-        for (int j = 0; j < 2; j++) {
-            if (j < g.edge && d2v[j] <= near && same_sqrt(d2v[j], best)) {
-                g.edge = j;
-                g.t = tv[j];
-                break;
-            }
-        }
+    const bool tie0 = g.edge > 0 && d2v[0] <= near, tie1 = g.edge > 1 && d2v[1] <= near;
+    if (__builtin_amdgcn_ballot_w64(tie0 || tie1) != 0) {
+        const bool eq0 = same_sqrt(d2v[0], best), eq1 = same_sqrt(d2v[1], best);
+        const bool s0 = tie0 && eq0, s1 = !s0 && tie1 && eq1;
+        g.t = s0 ? tv[0] : (s1 ? tv[1] : g.t);
+        g.edge = s0 ? 0 : (s1 ? 1 : g.edge);
     }
     const int ed = g.edge;
     g.ax = pick3_lane(r, ed, R_V + 0, R_V + 2, R_V + 4);
@@ -704,11 +706,13 @@ __device__ inline Geo geometry(const Rec& r, Pix p) {
 // tile and the other two edge lines stay clear of it, so the signs of their
 // cross products are the same at every pixel (inner side when PLAN_INNER).
 enum : uint32_t { PLAN_GENERAL = 3, PLAN_INNER = 4 };
-// Entry bits 5-6: the byte offset, within the record's edge blocks, of the
-// plan's block (32 min(plan & 3, 2)), so that a sweep addresses it with one
-// bitwise and. Entry bit 7: the tile lies inside the triangle's box (no
-// per-pixel box test).
-enum : uint32_t { ENT_EB = 0x60, ENT_INBOX = 0x80 };
+// Entry bits 0-1: a single-edge plan (ENT_SINGLE: plan & 3 != PLAN_GENERAL),
+// or whole coverage (ENT_FULL), one bit each so that a sweep tests either with
+// one scalar bit test; neither: the general path. Bits 2-4: the plan. Bits
+// 5-6: the byte offset, within the record's edge blocks, of the plan's block
+// (32 min(plan & 3, 2)), so that a sweep addresses it with one bitwise and.
+// Bit 7: the tile lies inside the triangle's box (no per-pixel box test).
+enum : uint32_t { ENT_SINGLE = 0x1, ENT_FULL = 0x2, ENT_EB = 0x60, ENT_INBOX = 0x80 };
 
 // geometry<true> for a single-edge plan: the reference's distance to edge j
 // and its cross product, with the other edges' results known. The excluded
@@ -771,20 +775,36 @@ __device__ inline Geo geometry1(const Rec& r, const f8v& eb, Pix p, uint32_t pla
 // and on the plan are wave-uniform; the empty volatile asm keeps the compiler
 // from if-converting them, which would evaluate every variant every time.
 template <bool FAST>
-__device__ inline void exact_cov(const Rec& r, const f8v& eb, Pix p, uint32_t plan, float rsig, float sig, Geo& g,
+__device__ inline void exact_cov(const Rec& r, const f8v& eb, Pix p, uint32_t code, float rsig, float sig, Geo& g,
                                  float& cov) {
-    if (FAST && (r.i(R_FLAGS) & F_FAST)) {
-        if ((plan & 3u) != PLAN_GENERAL) {
-            g = geometry1(r, eb, p, plan);
-        } else {
-            asm volatile("");
-            g = geometry<true>(r, p);
-        }
+    // single-edge plans are given to F_FAST triangles only (build_list)
+    if (FAST && (code & ENT_SINGLE)) {
+        g = geometry1(r, eb, p, (code >> 2) & 7u);
+        cov = sigmoid_f<true>(g.sd * rsig);
+    } else if (FAST && (r.i(R_FLAGS) & F_FAST)) {
+        asm volatile("");
+        g = geometry<true>(r, p);
         cov = sigmoid_f<true>(g.sd * rsig);
     } else {
         asm volatile("");
         g = geometry<false>(r, p);
         cov = sigmoid_f<FAST>(FAST ? g.sd * rsig : g.sd / sig);
+    }
+}
+
+// The exact coverage at the lanes of `bandm` (`band`: this lane's bit), 1.0f
+// at the others. Every lane evaluates it, under a wave-uniform branch on
+// `bandm`, and the others discard theirs: a divergent branch would cost the
+// same vector issue (masked lanes issue alike) plus the exec-mask saves and
+// restores, and makes the compiler carry flags through the branches around it.
+template <bool FAST>
+__device__ inline void band_cov(const Rec& r, const f8v& eb, Pix p, uint32_t code, uint64_t bandm, bool band,
+                                float rsig, float sig, Geo& g, float& cov) {
+    cov = 1.0f;
+    if (bandm != 0) {
+        float c;
+        exact_cov<FAST>(r, eb, p, code, rsig, sig, g, c);
+        cov = band ? c : 1.0f;
     }
 }
 
@@ -873,16 +893,16 @@ enum : uint32_t { CLS_PARTIAL = 1, CLS_FULL = 2 };
 // until the candidates exceed 64 (so at most 128 = CH, the list's size) or
 // [k0, k1) ends, and *kend is where they stopped: the sparse candidates of
 // many chunks (small triangles) then share one classification pass and one
-// entry loop. Entries then number their triangles from k0 over up to k1 - k0
-// triangles, so only a caller that takes every triangle index from the
-// entries (not from a per-chunk accumulator row) may merge. The
+// entry loop. Entries then hold their triangles' indices (below 2^23, so
+// k << 8 fits the entry word) rather than offsets from k0, so only a caller
+// that takes every triangle index from the entries (not from a per-chunk
+// accumulator row) may merge. The
 // classification then also loads every field any of its branches reads up
 // front (one round trip instead of one per branch level; the other callers
 // keep the lazy loads, whose registers their occupancy needs).
 //
 // With `ilist` (merged lists only) [k0, k1) are positions in ilist, a list of
-// triangle indices in order, and entries hold the triangles' indices instead
-// of their offsets from k0.
+// triangle indices in order.
 template <bool MERGE = false>
 __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, int tx0, int ty0,
                                  int tx1, int ty1, float cx0, float cy0, float cx1, float cy1,
@@ -890,7 +910,7 @@ __device__ inline int build_list(const float* __restrict__ rec, int k0, int k1, 
                                  const int* __restrict__ ilist = nullptr) {
     static_assert(CH >= 128, "a merged list holds two passes of candidates");
     static_assert(R_FLAGS == R_BOX + 4, "the box tests read x0 y0 x1 y1 flags as five consecutive ints");
-    const int kbase = ilist ? 0 : k0;
+    const int kbase = MERGE ? 0 : k0;
     int nc = 0;
     if (MERGE) *kend = k1;
     for (int base2 = k0; base2 < k1; base2 += 128) {
@@ -1030,7 +1050,8 @@ classify:
         if (cls != 0) {
             const int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            list[pos] = (kl << 8) | extra | (min(plan & 3u, 2u) << 5) | (plan << 2) | cls;
+            const uint32_t kind = cls == CLS_FULL ? ENT_FULL : ((plan & 3u) != PLAN_GENERAL ? ENT_SINGLE : 0u);
+            list[pos] = (kl << 8) | extra | (min(plan & 3u, 2u) << 5) | (plan << 2) | kind;
         }
         count += (int)__popcll(mask);
     }
@@ -1054,7 +1075,7 @@ __device__ inline uint64_t pair_weight(const Rec& r, const f8v& eb, uint32_t ent
     // operations instead of per-lane 0/1 values, which the compiler widens a
     // combined condition into before taking its mask.
     uint64_t actm = validm;
-    if ((ent & 3u) == CLS_FULL) {
+    if (ent & ENT_FULL) {
         bandm = 0;
         w = alpha;
         return actm & lane_mask(!(w <= MIN_WEIGHT));
@@ -1063,7 +1084,7 @@ __device__ inline uint64_t pair_weight(const Rec& r, const f8v& eb, uint32_t ent
         actm &= lane_mask((unsigned)(x - r.i(R_BOX)) < (unsigned)(r.i(R_BOX + 2) - r.i(R_BOX))) &
                 lane_mask((unsigned)(y - r.i(R_BOX + 1)) < (unsigned)(r.i(R_BOX + 3) - r.i(R_BOX + 1)));
     // build_list gives a single-edge plan to fast-path triangles (F_FAST) only
-    if (FAST && ((ent >> 2) & 3u) != PLAN_GENERAL) {
+    if (FAST && (ent & ENT_SINGLE)) {
         // A single-edge plan holds for every pixel of the tile, so every lane
         // evaluates its edge: no classification and no divergent branch. A deep
         // pixel (more than 17 sigma + slack inside every edge line) gets
@@ -1083,8 +1104,8 @@ __device__ inline uint64_t pair_weight(const Rec& r, const f8v& eb, uint32_t ent
         asm volatile("");
         g = geometry<true>(r, p);
         cov = sigmoid_f<true>(g.sd * rsig);
-    } else if (__builtin_amdgcn_inverse_ballot_w64(bandm)) {
-        exact_cov<FAST>(r, eb, p, (ent >> 2) & 7u, rsig, sig, g, cov);
+    } else {
+        band_cov<FAST>(r, eb, p, ent, bandm, __builtin_amdgcn_inverse_ballot_w64(bandm), rsig, sig, g, cov);
     }
     w = alpha * cov;
     // `bandm` hands the backward pass the lanes whose coverage it must evaluate:
@@ -1286,6 +1307,7 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
     const int cap2 = a.cap2;
     // wave-uniform: the entry stores address from a scalar base
     TileEnt* te = a.tl_ent + (size_t)uniform_u32((uint32_t)tg.tile) * cap2 + ent_off;
+    const TileEnt* const te0 = te;
     // Split backward: before recorded entry (c + 1) seg_m the pixel state goes to
     // checkpoint c of this tile, the start of the backward's segment c + 1 (of
     // the blocks the backward splits: those ranked below nsplit, or all
@@ -1312,7 +1334,7 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
         int count = tg.live ? build_list<MERGE>(rec, k0, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
                                                 tg.cx1, tg.cy1, lw, lane, F_LIVE, &k1, ilist)
                             : 0;
-        const int kbase = ilist ? 0 : k0;
+        const int kbase = MERGE ? 0 : k0;
         // the list one half (64 entries) at a time, one entry per lane: each
         // iteration takes its entry from its lane (v_readlane) instead of an LDS
         // read, its address arithmetic and its wait
@@ -1376,7 +1398,7 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                         // stores the same (wave-uniform) entry: no lane mask to set up
                         if (MERGE || (n2 < cap2 && lane == 0)) {
                             TileEnt e;
-                            e.k = ent + ((uint32_t)kbase << 8);  // (k << 8) | the entry's low byte
+                            e.k = MERGE ? ent : ent + ((uint32_t)kbase << 8);  // (k << 8) | the entry's low byte
                             // the merged lists' consumer reads no row
                             e.row = MERGE ? 0u : (ent >> 8) * (uint32_t)(NP * sizeof(float));
                             e.on = tapedm;
@@ -1387,13 +1409,14 @@ __device__ __forceinline__ void forward_sweep(const RasterArgs& a, const float* 
                         // instead of an index's 64-bit multiply-add. With the constant row
                         // -1.4 us of ~88 at B=16 256x256 T=128, with the rest -1.3 more
                         te++;
-                        n2++;
+                        if (!MERGE) n2++;  // merged lists: from the pointer at the end
                     }
                 }
             }
         }
-        if (n2 > cap2 && rec_chunks == n_chunks) rec_chunks = c;
+        if (!MERGE && n2 > cap2 && rec_chunks == n_chunks) rec_chunks = c;
     }
+    if (MERGE) n2 = (int)(te - te0);
 }
 
 template <int MODE, bool FAST, bool CKPT>
@@ -1502,28 +1525,30 @@ __device__ inline void grad_pixel(const Rec& r, bool on, bool band, bool any_ban
     if (!any_band) return;
     const float d_cov = d_w * r.f(R_A);
     // grad.rs:252-268: vertex terms, zero exactly on the boundary.
-    if (band && g.dist >= 1e-9f) {
-        // u = (pt - cp) / dist with cp = a + t (b - a), rounded as
-        // grad.rs:256-259 does: for a pixel within ~1e-7 of an edge the
-        // direction is set by these roundings, and the reference's gradient
-        // inherits them.
-        float inv = __builtin_amdgcn_rcpf(g.dist);
-        float cpx = g.ax + g.t * g.ex, cpy = g.ay + g.t * g.ey;
-        float ux = (p.px - cpx) * inv, uy = (p.py - cpy) * inv;
-        float chain = d_cov * cov * (1.0f - cov) * rsig;
-        chain = g.sd > 0.0f ? chain : -chain;
-        float A = -(1.0f - g.t) * chain;  // onto the edge's first vertex
-        float Bc = -g.t * chain;           // onto its second vertex
-        float s0 = g.edge == 0 ? A : (g.edge == 2 ? Bc : 0.0f);
-        float s1 = g.edge == 1 ? A : (g.edge == 0 ? Bc : 0.0f);
-        float s2 = g.edge == 2 ? A : (g.edge == 1 ? Bc : 0.0f);
-        a[0] = s0 * ux;
-        a[1] = s0 * uy;
-        a[2] = s1 * ux;
-        a[3] = s1 * uy;
-        a[4] = s2 * ux;
-        a[5] = s2 * uy;
-    }
+    // Every lane evaluates them (no divergent branch: the wave runs this block
+    // only for entries with band lanes, where the masked lanes would issue
+    // alike) and the lanes off the band or on the boundary take zeros.
+    const bool vt = band && g.dist >= 1e-9f;
+    // u = (pt - cp) / dist with cp = a + t (b - a), rounded as
+    // grad.rs:256-259 does: for a pixel within ~1e-7 of an edge the
+    // direction is set by these roundings, and the reference's gradient
+    // inherits them.
+    float inv = __builtin_amdgcn_rcpf(g.dist);
+    float cpx = g.ax + g.t * g.ex, cpy = g.ay + g.t * g.ey;
+    float ux = (p.px - cpx) * inv, uy = (p.py - cpy) * inv;
+    float chain = d_cov * cov * (1.0f - cov) * rsig;
+    chain = g.sd > 0.0f ? chain : -chain;
+    float A = -(1.0f - g.t) * chain;  // onto the edge's first vertex
+    float Bc = -g.t * chain;           // onto its second vertex
+    float s0 = g.edge == 0 ? A : (g.edge == 2 ? Bc : 0.0f);
+    float s1 = g.edge == 1 ? A : (g.edge == 0 ? Bc : 0.0f);
+    float s2 = g.edge == 2 ? A : (g.edge == 1 ? Bc : 0.0f);
+    a[0] = vt ? s0 * ux : 0.0f;
+    a[1] = vt ? s0 * uy : 0.0f;
+    a[2] = vt ? s1 * ux : 0.0f;
+    a[3] = vt ? s1 * uy : 0.0f;
+    a[4] = vt ? s2 * ux : 0.0f;
+    a[5] = vt ? s2 * uy : 0.0f;
 }
 
 // Wave sum of the lanes' partial gradients of one triangle, added to its row
@@ -1599,9 +1624,9 @@ __device__ __forceinline__ void backward_sweep(const RasterArgs& a, const float*
             Rec r;
             f8v eb;
             load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
-            float cov = 1.0f;
+            float cov;
             Geo g;
-            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            band_cov<FAST>(r, eb, tg.p, cur.k, cur.band, band, rsig, sig, g, cov);
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
@@ -2030,27 +2055,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void fu
     st.tot = tot;
     st.pre = {1.0f, 0, 0};
     const bool plain = lane_mask(tot.z != 0 || tot.e != 0) == 0;
-    const int cap2 = a.cap2;
-    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * cap2;
+    const TileEnt* __restrict__ te = ents + (size_t)uniform_u32((uint32_t)tg.tile) * a.cap2;
     float* const grads = a.grads + (size_t)b * T * NP;
     lds_float* const tw = (lds_float*)trans;
+    // The entry after the last one read is at byte offset `end`, inside the
+    // tile's region (cap2 > T >= n2 for this kernel): the loop prefetches it
+    // unclamped, and its byte offset is the loop's only counter.
+    const uint32_t end = (uint32_t)n2 * (uint32_t)sizeof(TileEnt);
     // The recorded entries in scene order (backward_sweep's recorded loop, with
     // every chunk at once: the gradient rows are global).
     auto sweep = [&](auto plain_c) {
         constexpr bool PLAIN = decltype(plain_c)::value;
         TileEnt nx = te[0];
-        for (int i2 = 0; i2 < n2; i2++) {
+        for (uint32_t off = 0; off < end;) {
             const TileEnt cur = nx;
             const int k = (int)(cur.k >> 8);
-            nx = ent_at(te, min(i2 + 1, cap2 - 1));
+            off += (uint32_t)sizeof(TileEnt);
+            nx = *reinterpret_cast<const TileEnt*>(reinterpret_cast<const char*>(te) + off);
             const bool on = __builtin_amdgcn_inverse_ballot_w64(cur.on);
             const bool band = __builtin_amdgcn_inverse_ballot_w64(cur.band);
             Rec r;
             f8v eb;
             load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
-            float cov = 1.0f;
+            float cov;
             Geo g;
-            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            band_cov<FAST>(r, eb, tg.p, cur.k, cur.band, band, rsig, sig, g, cov);
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);
@@ -2148,7 +2177,6 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
         const int count = tg.live ? build_list<true>(rec, kb, k1, tg.tx0, tg.ty0, tg.tx1, tg.ty1, tg.cx0, tg.cy0,
                                                      tg.cx1, tg.cy1, list[s], lane, F_LIVE, &kend)
                                   : 0;
-        const int kbase = kb;
         kb = tg.live ? kend : k1;
         // the list one half at a time, one entry per lane (as forward_sweep)
         for (int h = 0; h < count; h += 64) {
@@ -2156,7 +2184,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             const int nh = (int)uniform_u32((uint32_t)min(count - h, 64));
             for (int i = 0; i < nh; i++) {
                 const uint32_t ent = (uint32_t)__builtin_amdgcn_readlane((int)held, i);
-                const int k = kbase + (int)(ent >> 8);
+                const int k = (int)(ent >> 8);  // merged lists hold the triangle index
                 Rec r;
                 f8v eb;
                 load_entry<FAST, true>(rec, rec_off((uint32_t)k), ent, r, eb);
@@ -2175,7 +2203,7 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
                     e.on[0] = (uint32_t)onm;
                     e.on[1] = (uint32_t)(onm >> 32);
                     TileEnt t;
-                    t.k = ((uint32_t)k << 8) | (ent & 0xFFu);
+                    t.k = ent;
                     t.row = 0;
                     t.on = onm;
                     t.band = onm & bandm;
@@ -2274,9 +2302,9 @@ __global__ __launch_bounds__(S * 64) void fused_seg_kernel(RasterArgs a, const f
             Rec r;
             f8v eb;
             load_entry<FAST, true>(rec, rec_off((uint32_t)k), cur.k, r, eb);
-            float cov = 1.0f;
+            float cov;
             Geo g;
-            if (band) exact_cov<FAST>(r, eb, tg.p, (cur.k >> 2) & 7u, rsig, sig, g, cov);
+            band_cov<FAST>(r, eb, tg.p, cur.k, cur.band, band, rsig, sig, g, cov);
             const float w = r.f(R_A) * cov;
             float part[NP];
             grad_pixel<PLAIN>(r, on, band, cur.band != 0, w, cov, g, tg.p, rsig, st, part);

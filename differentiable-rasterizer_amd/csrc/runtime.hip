@@ -303,7 +303,10 @@ bool use_order(const drh_ctx* ctx, int B, int gx, int gy) {
 }
 
 bool fused_gradients(int mode, int nseg, int cap2, int T) {
-    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || nseg > 1 || cap2 < T || cap2 % 8 != 0)
+    // cap2 > T: the one-wave kernel's backward loop reads the slot after a
+    // tile's last entry (at most T of them); the segmented kernel's regions
+    // are sized alike
+    if ((mode != drh::MODE_LOSS && mode != drh::MODE_GRAD_IN) || nseg > 1 || cap2 <= T || cap2 % 8 != 0)
         return false;
     const char* e = std::getenv("DRH_UNFUSED");
     return !(e && e[0] == '1');
@@ -423,8 +426,9 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     const size_t ntiles = (size_t)B * nblk * drh::WAVES;
     Lease rec, partials, ploss, pq, pg0, pze, tent, tn, order, ckpt, rows;
     RasterBufs bufs;
-    // whole 64-byte lines per tile (8 entries), as the fused kernel needs
-    bufs.cap2 = tile_entries(ntiles, (T + 7) & ~7);
+    // whole 64-byte lines per tile (8 entries) and one slot past T entries, as
+    // the fused kernel needs
+    bufs.cap2 = tile_entries(ntiles, (T + 8) & ~7);
     // the records: the fit's own (FitTail::rec), else pooled
     int rc = tail && tail->rec ? DRH_OK : rec.acquire(ctx, K_REC, (size_t)B * T * drh::REC * sizeof(float), s);
     if (rc) return rc;
@@ -445,7 +449,7 @@ int run_raster(drh_ctx* ctx, int mode, const float* params, const float* bgs, co
     if (bufs.fused && use_segments(mode, ntiles, T)) {
         // each wave's region whole 64-byte lines
         bufs.segw = drh::SEG_WAVES;
-        bufs.cap2 = drh::SEG_WAVES * (((T + drh::SEG_WAVES - 1) / drh::SEG_WAVES + 7) & ~7);
+        bufs.cap2 = drh::seg_cap2(T);
     }
     if (ordered) {
         // the one-wave fused kernel takes an order of tiles where its cells fit

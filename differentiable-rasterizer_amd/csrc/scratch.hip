@@ -86,7 +86,7 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     L.order = off;
     if (L.ordered) off = up(off + (size_t)B * nblk * sizeof(int));
     // the call takes fused_seg_kernel where drh_fused_loss_backward would
-    const int seg_cap2 = drh::SEG_WAVES * (((T + drh::SEG_WAVES - 1) / drh::SEG_WAVES + 7) & ~7);
+    const int seg_cap2 = drh::seg_cap2((int)T);
     L.segw = use_segments(drh::MODE_LOSS, ntiles, T) && fused_gradients(drh::MODE_LOSS, 1, seg_cap2, T)
                  ? drh::SEG_WAVES
                  : 0;
@@ -94,7 +94,8 @@ ScratchLayout scratch_layout(const drh_ctx* ctx, int B, int T, int H, int W, boo
     if (det) off = up(off + (size_t)B * nblk * (L.segw ? drh::WAVES : 1) * T * NP * sizeof(float));
     L.tent = off;
     const size_t left = SCRATCH_BYTES > off ? SCRATCH_BYTES - off : 0;
-    L.cap2 = tile_entries(ntiles, (T + 7) & ~7, left, 1);  // whole 64-byte lines per tile, as the fused kernel needs
+    // whole 64-byte lines per tile and one slot past T entries, as the fused kernel needs
+    L.cap2 = tile_entries(ntiles, (T + 8) & ~7, left, 1);
     if (L.segw && (size_t)seg_cap2 * ntiles * sizeof(drh::TileEnt) <= left)
         L.cap2 = seg_cap2;
     else
